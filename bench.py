@@ -1,0 +1,306 @@
+"""Benchmark of the INT4-KV decode path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload ns|c2|c4|c5|c1] [--no-cpu-baseline]
+
+A step is one decode token through every layer of the workload: per layer,
+quantize-append the new token's K and V into that layer's INT4 cache (in
+place, HIP) and run the fused GQA decode attention over the whole context
+(HIP). Each layer has its own cache buffers, so a step streams
+layers x (cache bytes) from HBM — 576 MiB for the default workload, more than
+the 256 MB Infinity Cache holds. The step is captured once in a HIP graph and
+replayed; K replays are timed between two events after a device sync.
+
+Default workload "ns": Llama-3.1-8B attention shape (32 query heads, 8 KV
+heads, head dim 128, group 32, bf16) at 16K context, 32 layers. Printed: one
+JSON line with whole-job algorithmic GB/s (`value`), ms per token, the
+attention kernel's roofline (algorithmic bytes / average launch time from HIP
+events around every launch, vs 8 TB/s), and the CPU baseline (the C
+restatement of the reference's CPU path, timed on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "kv-cache-triton_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "INT4-KV decode attn HBM GB/s (% of peak); ms/token, Llama-3.1-8B shape 16K ctx"
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (B, Hq, Hkv, D, G, ctx, layers, dtype, ragged)
+    "ns": dict(B=1, Hq=32, Hkv=8, D=128, G=32, ctx=16384, layers=32, dtype="bf16", ragged=False,
+               desc="llama3.1-8b-decode-16k"),
+    "c2": dict(B=1, Hq=32, Hkv=8, D=128, G=32, ctx=4096, layers=32, dtype="bf16", ragged=False,
+               desc="llama3.1-8b-decode-4k"),
+    "c4": dict(B=8, Hq=64, Hkv=8, D=128, G=32, ctx=32768, layers=80, dtype="bf16", ragged=False,
+               desc="llama3.1-70b-shape-b8-decode-32k"),
+    "c5": dict(B=16, Hq=25, Hkv=25, D=64, G=32, ctx=1024, layers=48, dtype="f16", ragged=True,
+               desc="gpt2-xl-ragged-b16-decode"),
+    "c1": dict(B=1, Hq=12, Hkv=12, D=64, G=32, ctx=1024, layers=12, dtype="f32", ragged=False,
+               desc="gpt2-small-decode-1k"),
+}
+
+
+def scale_bytes(dtype: str) -> int:
+    return 4 if dtype == "f32" else 2
+
+
+def attn_bytes(w: dict, kv_tokens: int) -> int:
+    """Algorithmic HBM bytes of one decode-attention launch: packed K+V codes
+    and scales of every attended token, plus q in and o out."""
+    ng = -(-w["D"] // w["G"])
+    s_sz = 2  # bf16 scales (Llama) or fp16 scales (GPT-2)
+    q_sz = 4 if w["dtype"] == "f32" else 2
+    return (w["Hkv"] * kv_tokens * (w["D"] + 2 * ng * s_sz)
+            + w["B"] * w["Hq"] * w["D"] * 2 * q_sz)
+
+
+def append_bytes(w: dict) -> int:
+    ng = -(-w["D"] // w["G"])
+    x_sz = 4 if w["dtype"] == "f32" else 2
+    return w["B"] * w["Hkv"] * (2 * w["D"] * x_sz + w["D"] + 2 * ng * 2)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="ns", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=0, help="override the workload's layer count")
+    ap.add_argument("--ctx", type=int, default=0, help="override the workload's context length")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a HIP graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); the INT4 decode "
+              "path is measured on one MI355X. See the sharding note in DESIGN.md.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from kvint4 import ops
+
+    w = dict(WORKLOADS[args.workload])
+    if args.layers:
+        w["layers"] = args.layers
+    if args.ctx:
+        w["ctx"] = args.ctx
+    B, Hq, Hkv, D, G, ctx, L = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"], w["layers"]
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w["dtype"]]
+    sdt = torch.float16 if w["dtype"] != "bf16" else torch.bfloat16  # GPT-2: fp16 scales
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    S_cap = ctx + 1
+    W_ = ops.packed_width(D, G)
+    NG = ops.num_groups(D, G)
+
+    # ---- synthetic per-layer caches, filled by the HIP quantizer ----
+    seq_lens = None
+    if w["ragged"]:
+        lens = torch.randint(128, ctx + 1, (B,), generator=torch.Generator().manual_seed(4))
+        seq_lens = lens.to(dev, torch.int32)
+    layers = []
+    with torch.cuda.stream(stream):
+        for _ in range(L):
+            kp = torch.empty(B, Hkv, S_cap, W_, dtype=torch.uint8, device=dev)
+            vp = torch.empty_like(kp)
+            ks = torch.empty(B, Hkv, S_cap, NG, dtype=sdt, device=dev)
+            vs = torch.empty_like(ks)
+            for packed, scales in ((kp, ks), (vp, vs)):
+                x = torch.randn(B, Hkv, ctx, D, generator=gen, device=dev, dtype=torch.float32).to(tdt)
+                ops.quantize_into(x, packed, scales, G, 0)
+                del x
+            layer = dict(
+                kp=kp, ks=ks, vp=vp, vs=vs,
+                knew=torch.randn(B, Hkv, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
+                vnew=torch.randn(B, Hkv, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
+                q=torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
+                out=torch.empty(B, Hq, 1, D, device=dev, dtype=tdt),
+            )
+            layers.append(layer)
+    torch.cuda.synchronize()
+
+    pos = seq_lens if seq_lens is not None else ctx
+    attended = ctx + 1
+    sm_scale = D ** -0.5
+
+    # ragged: each sequence attends its own length plus the new token
+    seq_plus = (seq_lens + 1) if seq_lens is not None else None
+
+    def attn(layer):
+        ops.fused_decode_attention(
+            layer["q"], layer["kp"][:, :, :attended], layer["ks"][:, :, :attended],
+            layer["vp"][:, :, :attended], layer["vs"][:, :, :attended],
+            n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm_scale,
+            seq_lens=seq_plus, out=layer["out"],
+        )
+
+    def step():
+        for layer in layers:
+            ops.quantize_into(layer["knew"], layer["kp"], layer["ks"], G, pos)
+            ops.quantize_into(layer["vnew"], layer["vp"], layer["vs"], G, pos)
+            attn(layer)
+
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup)):
+            step()
+    torch.cuda.synchronize()
+    eager_out = [l["out"].clone() for l in layers]
+
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        torch.cuda.synchronize()
+        # every replay must reproduce the eager result
+        for _ in range(3):
+            with torch.cuda.stream(stream):
+                for l in layers:
+                    l["out"].zero_()
+                graph.replay()
+            torch.cuda.synchronize()
+            for l, ref in zip(layers, eager_out):
+                if not torch.equal(l["out"], ref):
+                    print("bench.py: graph replay differs from the eager step", file=sys.stderr)
+                    return 1
+
+    # ---- timed region: K steps ----
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            if graph is not None:
+                graph.replay()
+            else:
+                step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    # ---- attention kernel alone: HIP events around every launch ----
+    n_rep = max(2, min(args.steps, 10))
+    evs = []
+    with torch.cuda.stream(stream):
+        for _ in range(n_rep):
+            for layer in layers:
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                attn(layer)
+                b.record(stream)
+                evs.append((a, b))
+    torch.cuda.synchronize()
+    launch_us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    attn_us = float(launch_us.mean())
+
+    kv_tokens = int((seq_lens + 1).sum().item()) if seq_lens is not None else B * attended
+    a_bytes = attn_bytes(w, kv_tokens)
+    step_bytes = L * (a_bytes + append_bytes(w))
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = a_bytes / (attn_us * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w["dtype"],
+        "data": "synthetic (seeded torch.randn K/V/q, quantized in place by the HIP kernel)",
+        "config": {
+            "workload": w["desc"], "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
+            "group_size": G, "context": ctx, "layers": L, "ragged": w["ragged"],
+            "graph": graph is not None,
+        },
+        "ms_per_token": round(ms_per_step, 5),
+        "attn_us_per_layer": round(attn_us, 3),
+        "attn_us_per_layer_median": round(float(np.median(launch_us)), 3),
+        "kv_cache_mib": round(L * B * Hkv * attended * 2 * (W_ + NG * 2) / 2**20, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_attn_kernel",
+            "bytes_per_launch": a_bytes,
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, layers, attended, seq_lens, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(w: dict, layers: list, attended: int, seq_lens, budget_s: float) -> dict:
+    """Time the C restatement of the reference's CPU path (dequantize + SDPA
+    over the INT4 cache, plus the quantize-append) on the host cores, on as
+    many layers of the same workload as fit in `budget_s` seconds."""
+    import numpy as np
+
+    from oracle import kvq_ref as R
+
+    B, Hq, Hkv, D, G = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"]
+    threads = R.num_threads()
+    sample = layers[: max(1, min(len(layers), 4))]
+    host = []
+    for layer in sample:
+        n = attended
+        host.append(dict(
+            kp=layer["kp"][:, :, :n].cpu().numpy(), vp=layer["vp"][:, :, :n].cpu().numpy(),
+            ks=layer["ks"][:, :, :n].float().cpu().numpy(), vs=layer["vs"][:, :, :n].float().cpu().numpy(),
+            q=layer["q"].float().cpu().numpy(), knew=layer["knew"].float().cpu().numpy(),
+            vnew=layer["vnew"].float().cpu().numpy(),
+        ))
+    sl = None if seq_lens is None else (seq_lens + 1).cpu().numpy()
+    sdt = "bf16" if w["dtype"] == "bf16" else "f16"
+    done, t0 = 0, time.perf_counter()
+    while True:
+        h = host[done % len(host)]
+        R.quantize_int4(h["knew"], G, sdt)
+        R.quantize_int4(h["vnew"], G, sdt)
+        R.decode_attn(h["q"], h["kp"], h["ks"], h["vp"], h["vs"], group_size=G, scale=D ** -0.5,
+                      seq_lens=sl, threads=threads)
+        done += 1
+        if time.perf_counter() - t0 > budget_s and done >= 2:
+            break
+    dt = time.perf_counter() - t0
+    kv_tokens = int(sl.sum()) if sl is not None else B * attended
+    per = attn_bytes(w, kv_tokens) + append_bytes(w)
+    return {
+        "value": round(done * per / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{done} layer-steps ({w['desc']}, {len(host)} distinct layers cycled), "
+                  f"C restatement oracle/kvq_ref.c, OpenMP x{threads}, {dt:.1f} s",
+        "ms_per_layer": round(dt / done * 1e3, 3),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

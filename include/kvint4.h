@@ -1,0 +1,154 @@
+/*
+ * kvint4.h — C ABI of libkvint4.so, the gfx950 (MI355X) INT4 KV-cache decode path.
+ *
+ * Conventions shared by every entry point:
+ *   - Plain pointers and sizes only. All data pointers are device pointers
+ *     (HBM); the caller owns every allocation. No entry point allocates device
+ *     memory, synchronizes the stream, or touches the host except to read its
+ *     scalar arguments.
+ *   - Kernels are enqueued on `stream` (a hipStream_t passed as void*; NULL =
+ *     the null stream). Work is asynchronous with respect to the host.
+ *   - Return value: KVQ_OK (0) on success, a negative KVQ_E* code otherwise.
+ *     kvq_last_error() returns a thread-local, human-readable message for the
+ *     last failing call on the calling thread.
+ *   - dtype codes: KVQ_BF16, KVQ_F16, KVQ_F32.
+ *   - Strides are in elements of the tensor's own type, except for the packed
+ *     uint8 tensors whose strides are in bytes (same thing for uint8). The last
+ *     (innermost) dimension of packed codes and of scales must be contiguous.
+ *
+ * Storage format (identical to the reference's, bit for bit):
+ *   packed[..., j] : uint8, per group of `G` elements a run of ceil(G/2) bytes;
+ *                    element 2i of the group goes to the low nibble of byte i,
+ *                    element 2i+1 to the high nibble; code = round_half_even(
+ *                    x / scale) clamped to [-8, 7], plus 8. For odd G the last
+ *                    high nibble of each group is 0.
+ *   scales[..., g] : scale = max|x_g| / 7 (or 1 for an all-zero group), computed
+ *                    in fp32 and rounded to nearest-even into the scale dtype.
+ */
+#ifndef KVINT4_H
+#define KVINT4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum kvq_dtype { KVQ_BF16 = 0, KVQ_F16 = 1, KVQ_F32 = 2 };
+
+enum kvq_status {
+  KVQ_OK = 0,
+  KVQ_EINVAL = -1,   /* bad argument: shape, dtype, stride, group size, null pointer */
+  KVQ_ESPACE = -2,   /* workspace too small */
+  KVQ_EHIP = -3,     /* HIP runtime error (launch failure, no device) */
+  KVQ_EUNSUP = -4    /* shape valid but not handled by the fused kernel */
+};
+
+/* Library version: major*10000 + minor*100 + patch. */
+int kvq_version(void);
+
+/* Thread-local message describing the last error on this thread ("" if none). */
+const char* kvq_last_error(void);
+
+/*
+ * kvq_quantize — INT4 group quantize + pack, written in place.
+ *
+ * Replaces the quantizer of the reference:
+ *   kernels/llama3/quantize.py:189-207 quantize_int4 (and the CPU semantics it
+ *   must match, _quantize_int4_torch :126-148; scales in the input dtype), and
+ *   kernels/gpt2/quantize.py:174-187 (same codes, scales always fp16), plus the
+ *   append half of models/llama3/kv_cache.py:76-102 (which concatenates the new
+ *   rows onto the cache; here they are written straight into a preallocated one).
+ *
+ * x:        [B, H, S, D] of x_dtype, element strides x_strides[4] (b, h, s, d).
+ * packed:   destination codes, row stride layout [B, H, *, ceil(D/G)*ceil(G/2)],
+ *           byte strides packed_strides[3] (b, h, s); last dim contiguous.
+ * scales:   destination scales [B, H, *, ceil(D/G)] of scale_dtype, element
+ *           strides scale_strides[3] (b, h, s); last dim contiguous.
+ * Row (b, h, s) of x is written to destination row (b, h, pos_b + s) where
+ * pos_b = write_pos[b] when write_pos (device int32 [B]) is not NULL, else
+ * write_pos0. The caller guarantees the destination rows exist.
+ */
+int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides,
+                 int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
+                 void* packed, const int64_t* packed_strides,
+                 void* scales, int scale_dtype, const int64_t* scale_strides,
+                 const int32_t* write_pos, int64_t write_pos0,
+                 void* stream);
+
+/*
+ * kvq_dequantize — unpack + scale back to floating point.
+ *
+ * Replaces kernels/llama3/quantize.py:274-308 dequantize_int4 (CPU semantics
+ * :210-234: value = (nibble - 8) * float(scale), rounded once into out_dtype,
+ * truncated to d_out columns) and kernels/gpt2/quantize.py:190-214 (fp16 out).
+ *
+ * packed/scales: [B, H, S, ...] as written by kvq_quantize (strides as there).
+ * num_groups:    scales' last dimension; the packed row must hold
+ *                num_groups*ceil(G/2) bytes.
+ * out:           [B, H, S, d_out] of out_dtype, element strides out_strides[4];
+ *                d_out <= num_groups*G.
+ */
+int kvq_dequantize(const void* packed, const int64_t* packed_strides,
+                   const void* scales, int scale_dtype, const int64_t* scale_strides,
+                   int64_t B, int64_t H, int64_t S, int64_t group_size, int64_t num_groups,
+                   void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
+                   void* stream);
+
+/*
+ * Split-K planning for kvq_decode_attn. Pure host arithmetic (no device call):
+ * returns the number of sequence splits the fused kernel will use for this
+ * shape on a device with `num_cus` compute units (>= 1), or a negative status.
+ * `s_max` is the longest sequence (tokens) that will be attended.
+ */
+int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                                   int64_t D, int64_t s_max, int q_dtype, int64_t num_cus);
+
+/*
+ * Workspace (device bytes) kvq_decode_attn needs for `n_split` splits. The
+ * workspace must be zero-filled once before its first use; the kernel leaves
+ * its counters at zero again on exit, so it can be reused by later calls on the
+ * same stream. Calls that overlap in time must not share a workspace.
+ */
+int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                                        int64_t D, int q_dtype, int64_t n_split);
+
+/*
+ * kvq_decode_attn — fused INT4 GQA attention for short query blocks (decode).
+ *
+ * Replaces kernels/llama3/attention_quant.py:159-286 attention_forward_quant_gqa
+ * (kernel :24-152) and kernels/gpt2/attention_quant.py:140-248
+ * attention_forward_quant (the MHA case, Hq == Hkv) for the shapes the fused
+ * kernel handles (D in {32, 64, 128}, group_size a multiple of 32 dividing
+ * into D's 32-element chunks); KVQ_EUNSUP otherwise.
+ *
+ * q:    [B, Hq, Sq, D] of q_dtype, element strides q_strides[4].
+ * k_packed/v_packed: [B, Hkv, Sk, num_groups*G/2] uint8, byte strides [3].
+ * k_scales/v_scales: [B, Hkv, Sk, num_groups] of scale_dtype, strides [3].
+ * out:  [B, Hq, Sq, D] of q_dtype, element strides out_strides[4].
+ * Query head h reads KV head h / (Hq / Hkv). Keys of sequence b are the first
+ * L_b = min(seq_lens[b], Sk) rows (seq_lens: device int32 [B], or NULL for
+ * L_b = Sk). With is_causal, query row i may attend key j iff
+ * j <= L_b - Sq + i (bottom-right alignment, as the reference kernel). A row
+ * with no admissible key yields zeros. Scores are scaled by sm_scale.
+ * n_split must come from kvq_decode_attn_num_splits (or be >= 1); workspace must
+ * hold kvq_decode_attn_workspace_bytes(...) bytes (may be NULL when that is 0).
+ */
+int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_strides,
+                    const void* k_packed, const int64_t* kp_strides,
+                    const void* k_scales, const int64_t* ks_strides,
+                    const void* v_packed, const int64_t* vp_strides,
+                    const void* v_scales, const int64_t* vs_strides,
+                    int scale_dtype,
+                    void* out, const int64_t* out_strides,
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                    int64_t group_size, int64_t Sk,
+                    const int32_t* seq_lens, int is_causal, float sm_scale,
+                    int64_t n_split, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVINT4_H */

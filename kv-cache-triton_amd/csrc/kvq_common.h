@@ -1,0 +1,70 @@
+// Shared definitions for the gfx950 INT4 KV kernels: dtype codes, scalar
+// load/store with round-to-nearest-even narrowing, and the thread-local error
+// slot behind kvq_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kvint4.h"
+
+namespace kvq {
+
+// bf16 <-> fp32. Widening is exact (bf16 is the top half of an fp32 word).
+// Narrowing rounds to nearest, ties to even, like torch's Tensor.to(bfloat16);
+// NaN stays a quiet NaN.
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __builtin_bit_cast(float, h << 16);
+}
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Load element i of a tensor of dtype `dt` as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dt) {
+  if (dt == KVQ_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  if (dt == KVQ_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+
+// Store fp32 `v` into element i of a tensor of dtype `dt` (RNE narrowing).
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float v) {
+  if (dt == KVQ_BF16) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else if (dt == KVQ_F16) ((uint16_t*)p)[i] = (uint16_t)f32_to_f16_bits(v);
+  else ((float*)p)[i] = v;
+}
+
+inline int dtype_size(int dt) { return dt == KVQ_F32 ? 4 : 2; }
+inline bool dtype_ok(int dt) { return dt == KVQ_BF16 || dt == KVQ_F16 || dt == KVQ_F32; }
+
+// Thread-local error message (host side).
+void set_error(const char* fmt, ...);
+void clear_error();
+
+}  // namespace kvq
+
+#define KVQ_CHECK_ARG(cond, ...)          \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::kvq::set_error(__VA_ARGS__);      \
+      return KVQ_EINVAL;                  \
+    }                                     \
+  } while (0)
+
+#define KVQ_CHECK_LAUNCH(what)                                                   \
+  do {                                                                           \
+    hipError_t e_ = hipGetLastError();                                           \
+    if (e_ != hipSuccess) {                                                      \
+      ::kvq::set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e_)); \
+      return KVQ_EHIP;                                                           \
+    }                                                                            \
+  } while (0)

@@ -1,0 +1,200 @@
+// INT4 group quantize/pack (written in place into a cache slot) and dequantize.
+//
+// Semantics follow the reference's CPU path exactly:
+//   quantize:   kernels/llama3/quantize.py:126-148 (_quantize_int4_torch)
+//               kernels/gpt2/quantize.py:111-133 (same codes, fp16 scales)
+//   dequantize: kernels/llama3/quantize.py:210-234, kernels/gpt2/quantize.py:217-235
+// i.e. scale = max|x_g| / 7 in fp32 (1 for an all-zero group), code =
+// round_half_even(x / scale) (IEEE fp32 division) clamped to [-8, 7] plus 8,
+// element 2i -> low nibble of byte i, element 2i+1 -> high nibble, zero padding
+// of the last group when G does not divide D, and for odd G one zero nibble
+// closing each group. Dequant = (nibble - 8) * fp32(scale), narrowed once.
+//
+// One thread owns one (row, group): the group's absmax is a private loop, so
+// no cross-lane reduction is needed, and consecutive threads own consecutive
+// groups of the same row, which keeps the global accesses of a wave dense.
+
+#include "kvq_common.h"
+
+namespace kvq {
+
+struct QuantArgs {
+  const void* x;
+  int64_t xs_b, xs_h, xs_s, xs_d;   // element strides of x
+  int64_t H, S, D, G, ngroups, bpg; // bpg = bytes per group = ceil(G/2)
+  int64_t rows;                     // B*H*S
+  uint8_t* packed;
+  int64_t ps_b, ps_h, ps_s;         // byte strides of packed
+  void* scales;
+  int64_t ss_b, ss_h, ss_s;         // element strides of scales
+  const int32_t* write_pos;
+  int64_t write_pos0;
+  int x_dtype, scale_dtype;
+};
+
+template <int XDT>
+__device__ __forceinline__ float ld_x(const void* p, int64_t i) {
+  if constexpr (XDT == KVQ_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  else if constexpr (XDT == KVQ_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  else return ((const float*)p)[i];
+}
+
+template <int XDT>
+__global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.rows * a.ngroups) return;
+  const int64_t row = idx / a.ngroups;
+  const int64_t g = idx - row * a.ngroups;
+  const int64_t s = row % a.S;
+  const int64_t bh = row / a.S;
+  const int64_t h = bh % a.H;
+  const int64_t b = bh / a.H;
+
+  const int64_t xbase = b * a.xs_b + h * a.xs_h + s * a.xs_s;
+  const int64_t c0 = g * a.G;
+  const int64_t c1 = (c0 + a.G < a.D) ? c0 + a.G : a.D;  // real columns [c0, c1)
+
+  float amax = 0.0f;
+  for (int64_t c = c0; c < c1; ++c) amax = fmaxf(amax, fabsf(ld_x<XDT>(a.x, xbase + c * a.xs_d)));
+  // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
+  const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+
+  const int64_t pos = (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s;
+  uint8_t* prow = a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + g * a.bpg;
+
+  for (int64_t j = 0; j < a.bpg; ++j) {
+    uint32_t nib[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int64_t k = 2 * j + e;  // element index inside the group
+      if (k >= a.G) {               // odd G: the closing pad nibble is 0
+        nib[e] = 0u;
+        continue;
+      }
+      const int64_t c = c0 + k;
+      const float v = c < c1 ? ld_x<XDT>(a.x, xbase + c * a.xs_d) : 0.0f;
+      float qf = __builtin_rintf(v / scale);  // round half to even
+      qf = fminf(fmaxf(qf, -8.0f), 7.0f);
+      nib[e] = (uint32_t)((int)qf + 8);
+    }
+    prow[j] = (uint8_t)(nib[0] | (nib[1] << 4));
+  }
+  const int64_t sidx = b * a.ss_b + h * a.ss_h + pos * a.ss_s + g;
+  store_from_f32(a.scales, sidx, a.scale_dtype, scale);
+}
+
+struct DequantArgs {
+  const uint8_t* packed;
+  int64_t ps_b, ps_h, ps_s;
+  const void* scales;
+  int64_t ss_b, ss_h, ss_s;
+  int64_t H, S, G, ngroups, bpg, d_out, rows;
+  void* out;
+  int64_t os_b, os_h, os_s, os_d;
+  int scale_dtype, out_dtype;
+};
+
+__global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.rows * a.ngroups) return;
+  const int64_t row = idx / a.ngroups;
+  const int64_t g = idx - row * a.ngroups;
+  const int64_t s = row % a.S;
+  const int64_t bh = row / a.S;
+  const int64_t h = bh % a.H;
+  const int64_t b = bh / a.H;
+
+  const uint8_t* prow = a.packed + b * a.ps_b + h * a.ps_h + s * a.ps_s + g * a.bpg;
+  const float scale = load_as_f32(a.scales, b * a.ss_b + h * a.ss_h + s * a.ss_s + g, a.scale_dtype);
+  const int64_t obase = b * a.os_b + h * a.os_h + s * a.os_s;
+  for (int64_t k = 0; k < a.G; ++k) {
+    const int64_t c = g * a.G + k;
+    if (c >= a.d_out) break;
+    const uint32_t byte = prow[k >> 1];
+    const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
+    const float v = (float)((int)nib - 8) * scale;
+    store_from_f32(a.out, obase + c * a.os_d, a.out_dtype, v);
+  }
+}
+
+}  // namespace kvq
+
+using namespace kvq;
+
+extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides,
+                            int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
+                            void* packed, const int64_t* packed_strides,
+                            void* scales, int scale_dtype, const int64_t* scale_strides,
+                            const int32_t* write_pos, int64_t write_pos0,
+                            void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(group_size > 0, "kvq_quantize: group_size must be > 0");
+  KVQ_CHECK_ARG(dtype_ok(x_dtype), "kvq_quantize: x dtype must be bf16/fp16/fp32");
+  KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_quantize: scale dtype must be bf16/fp16/fp32");
+  KVQ_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D >= 0, "kvq_quantize: negative extent");
+  KVQ_CHECK_ARG(x_strides && packed_strides && scale_strides, "kvq_quantize: null stride array");
+  KVQ_CHECK_ARG(write_pos0 >= 0, "kvq_quantize: write_pos0 must be >= 0");
+  const int64_t rows = B * H * S;
+  const int64_t ngroups = (D + group_size - 1) / group_size;
+  if (rows == 0 || ngroups == 0) return KVQ_OK;
+  KVQ_CHECK_ARG(x && packed && scales, "kvq_quantize: null data pointer");
+
+  QuantArgs a;
+  a.x = x;
+  a.xs_b = x_strides[0]; a.xs_h = x_strides[1]; a.xs_s = x_strides[2]; a.xs_d = x_strides[3];
+  a.H = H; a.S = S; a.D = D; a.G = group_size; a.ngroups = ngroups; a.bpg = (group_size + 1) / 2;
+  a.rows = rows;
+  a.packed = (uint8_t*)packed;
+  a.ps_b = packed_strides[0]; a.ps_h = packed_strides[1]; a.ps_s = packed_strides[2];
+  a.scales = scales;
+  a.ss_b = scale_strides[0]; a.ss_h = scale_strides[1]; a.ss_s = scale_strides[2];
+  a.write_pos = write_pos; a.write_pos0 = write_pos0;
+  a.x_dtype = x_dtype; a.scale_dtype = scale_dtype;
+
+  const int64_t total = rows * ngroups;
+  const dim3 block(256);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (x_dtype) {
+    case KVQ_BF16: hipLaunchKernelGGL(quantize_kernel<KVQ_BF16>, grid, block, 0, st, a); break;
+    case KVQ_F16: hipLaunchKernelGGL(quantize_kernel<KVQ_F16>, grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL(quantize_kernel<KVQ_F32>, grid, block, 0, st, a); break;
+  }
+  KVQ_CHECK_LAUNCH("kvq_quantize");
+  return KVQ_OK;
+}
+
+extern "C" int kvq_dequantize(const void* packed, const int64_t* packed_strides,
+                              const void* scales, int scale_dtype, const int64_t* scale_strides,
+                              int64_t B, int64_t H, int64_t S, int64_t group_size, int64_t num_groups,
+                              void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
+                              void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(group_size > 0, "kvq_dequantize: group_size must be > 0");
+  KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_dequantize: scale dtype must be bf16/fp16/fp32");
+  KVQ_CHECK_ARG(dtype_ok(out_dtype), "kvq_dequantize: out dtype must be bf16/fp16/fp32");
+  KVQ_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && num_groups >= 0 && d_out >= 0,
+                "kvq_dequantize: negative extent");
+  KVQ_CHECK_ARG(d_out <= num_groups * group_size, "kvq_dequantize: d_out exceeds num_groups*group_size");
+  KVQ_CHECK_ARG(packed_strides && scale_strides && out_strides, "kvq_dequantize: null stride array");
+  const int64_t rows = B * H * S;
+  if (rows == 0 || num_groups == 0 || d_out == 0) return KVQ_OK;
+  KVQ_CHECK_ARG(packed && scales && out, "kvq_dequantize: null data pointer");
+
+  DequantArgs a;
+  a.packed = (const uint8_t*)packed;
+  a.ps_b = packed_strides[0]; a.ps_h = packed_strides[1]; a.ps_s = packed_strides[2];
+  a.scales = scales;
+  a.ss_b = scale_strides[0]; a.ss_h = scale_strides[1]; a.ss_s = scale_strides[2];
+  a.H = H; a.S = S; a.G = group_size; a.ngroups = num_groups; a.bpg = (group_size + 1) / 2;
+  a.d_out = d_out; a.rows = rows;
+  a.out = out;
+  a.os_b = out_strides[0]; a.os_h = out_strides[1]; a.os_s = out_strides[2]; a.os_d = out_strides[3];
+  a.scale_dtype = scale_dtype; a.out_dtype = out_dtype;
+
+  const int64_t total = rows * num_groups;
+  hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  KVQ_CHECK_LAUNCH("kvq_dequantize");
+  return KVQ_OK;
+}

@@ -1,0 +1,209 @@
+"""Storage engine shared by the Llama-3 and GPT-2 ``QuantizedKVCache`` classes.
+
+The reference appends by ``torch.cat`` of the whole layer cache on every step
+(``models/llama3/kv_cache.py:96-101``), moving O(S) bytes per token. Here each
+layer owns preallocated capacity buffers
+
+    k_packed, v_packed : [B, H_kv, capacity, packed_width]   uint8
+    k_scales, v_scales : [B, H_kv, capacity, n_groups]       scale dtype
+
+and new tokens are quantized by the HIP kernel straight into rows
+[seq_len, seq_len + S). Capacity grows geometrically (one copy per doubling).
+``get_quantized`` returns ``[:, :, :seq_len]`` views: same shapes and values as
+the reference's tensors, no copy.
+
+Ragged batches (per-sequence lengths, not in the reference) are supported by
+``load_ragged`` + ``append``: sequence b's new rows go to positions
+seq_lens[b] + s (a device int32 tensor updated in place), and the attention
+kernel masks keys past each sequence's length.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import ops
+
+_ROUND = 256  # capacity granularity (tokens)
+
+
+@dataclass
+class _LayerQuantizedKV:
+    """Per-layer state. Field names follow the reference
+    (models/llama3/kv_cache.py:21-27); the tensors may hold more rows than
+    ``seq_len`` (capacity). ``seq_lens`` is set only for ragged layers."""
+
+    k_packed: torch.Tensor
+    k_scales: torch.Tensor
+    v_packed: torch.Tensor
+    v_scales: torch.Tensor
+    seq_len: int
+    seq_lens: Optional[torch.Tensor] = None
+
+    @property
+    def capacity(self) -> int:
+        return int(self.k_packed.shape[2])
+
+
+def _round_up(n: int, m: int) -> int:
+    return (n + m - 1) // m * m
+
+
+class QuantizedKVCacheBase:
+    """Family-independent part of the INT4 cache. Subclasses set
+    ``_scale_dtype_for(x)`` and ``_deq_dtype_default``."""
+
+    def __init__(self, group_size: int = 32, reserve_tokens: int = 0):
+        if group_size <= 0:
+            raise ValueError("group_size must be > 0")
+        self.group_size = int(group_size)
+        self.reserve_tokens = int(reserve_tokens)
+        self._layers: dict[int, _LayerQuantizedKV] = {}
+
+    # -- family policy -------------------------------------------------------
+    def _scale_dtype_for(self, x: torch.Tensor) -> torch.dtype:  # pragma: no cover
+        raise NotImplementedError
+
+    # -- HF cache protocol ---------------------------------------------------
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        layer = self._layers.get(layer_idx)
+        return 0 if layer is None else int(layer.seq_len)
+
+    def get_query_offset(self, layer_idx: int = 0) -> int:
+        """transformers>=5 masking: first position of the incoming queries."""
+        return self.get_seq_length(layer_idx)
+
+    @property
+    def is_initialized(self) -> bool:
+        return len(self._layers) > 0
+
+    @property
+    def is_sliding(self) -> list[bool]:
+        return [False for _ in self._layers]
+
+    is_compileable = False
+
+    def __len__(self) -> int:
+        return len(self._layers)
+
+    def reset(self) -> None:
+        self._layers.clear()
+
+    def has_layer(self, layer_idx: int) -> bool:
+        return layer_idx in self._layers
+
+    # -- storage -------------------------------------------------------------
+    def _alloc(self, like: torch.Tensor, B: int, H: int, cap: int, D: int, scale_dtype: torch.dtype):
+        w = ops.packed_width(D, self.group_size)
+        ng = ops.num_groups(D, self.group_size)
+        dev = like.device
+        return (
+            torch.empty((B, H, cap, w), dtype=torch.uint8, device=dev),
+            torch.empty((B, H, cap, ng), dtype=scale_dtype, device=dev),
+            torch.empty((B, H, cap, w), dtype=torch.uint8, device=dev),
+            torch.empty((B, H, cap, ng), dtype=scale_dtype, device=dev),
+        )
+
+    def _ensure_layer(self, key_states: torch.Tensor, layer_idx: int, needed: int) -> _LayerQuantizedKV:
+        B, H, _, D = key_states.shape
+        scale_dtype = self._scale_dtype_for(key_states)
+        layer = self._layers.get(layer_idx)
+        if layer is None:
+            cap = _round_up(max(needed + max(_ROUND, needed // 8), self.reserve_tokens), _ROUND)
+            kp, ks, vp, vs = self._alloc(key_states, B, H, cap, D, scale_dtype)
+            layer = _LayerQuantizedKV(kp, ks, vp, vs, 0)
+            self._layers[layer_idx] = layer
+            return layer
+        if layer.k_packed.shape[:2] != (B, H) or layer.k_packed.shape[-1] != ops.packed_width(D, self.group_size):
+            raise ValueError(
+                f"layer {layer_idx}: new K/V shape {tuple(key_states.shape)} does not match the cache "
+                f"(B={layer.k_packed.shape[0]}, H={layer.k_packed.shape[1]})"
+            )
+        if layer.k_scales.dtype != scale_dtype:
+            raise ValueError(f"layer {layer_idx}: scale dtype {scale_dtype} differs from the cache's")
+        if needed > layer.capacity:
+            cap = _round_up(max(needed, 2 * layer.capacity), _ROUND)
+            kp, ks, vp, vs = self._alloc(key_states, B, H, cap, D, scale_dtype)
+            n = layer.seq_len
+            for dst, src in ((kp, layer.k_packed), (ks, layer.k_scales), (vp, layer.v_packed), (vs, layer.v_scales)):
+                dst[:, :, :n].copy_(src[:, :, :n])
+            layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales = kp, ks, vp, vs
+        return layer
+
+    def _append_quantized(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> None:
+        if key_states.shape != value_states.shape:
+            raise ValueError("key_states and value_states must have the same shape")
+        if key_states.dim() != 4:
+            raise ValueError("key/value states must be [B, H_kv, S, d_head]")
+        S = int(key_states.shape[2])
+        prev = self._layers.get(layer_idx)
+        start = 0 if prev is None else prev.seq_len
+        layer = self._ensure_layer(key_states, layer_idx, start + S)
+        pos = layer.seq_lens if layer.seq_lens is not None else start
+        ops.quantize_into(key_states, layer.k_packed, layer.k_scales, self.group_size, pos)
+        ops.quantize_into(value_states, layer.v_packed, layer.v_scales, self.group_size, pos)
+        if layer.seq_lens is not None:
+            layer.seq_lens.add_(S)
+        layer.seq_len = start + S
+
+    def append(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> None:
+        """Quantize [B, H_kv, S, d] K/V and append them to layer `layer_idx`."""
+        self._append_quantized(key_states, value_states, layer_idx)
+
+    def load_ragged(
+        self,
+        key_states: torch.Tensor,
+        value_states: torch.Tensor,
+        layer_idx: int,
+        lengths: torch.Tensor,
+    ) -> None:
+        """Start a ragged layer from padded K/V [B, H_kv, S_max, d] whose
+        sequence b holds `lengths[b]` valid rows. Later `append` calls write
+        each sequence's new rows right after its own last row."""
+        if layer_idx in self._layers:
+            raise ValueError(f"layer {layer_idx} already holds state")
+        if lengths.numel() != key_states.shape[0]:
+            raise ValueError("lengths must have one entry per batch row")
+        self._append_quantized(key_states, value_states, layer_idx)
+        layer = self._layers[layer_idx]
+        layer.seq_lens = lengths.to(device=key_states.device, dtype=torch.int32).clone()
+
+    def get_seq_lens(self, layer_idx: int) -> Optional[torch.Tensor]:
+        """Per-sequence lengths of a ragged layer (device int32 [B]) or None."""
+        layer = self._layers.get(layer_idx)
+        return None if layer is None else layer.seq_lens
+
+    def get_quantized(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        layer = self._layers.get(layer_idx)
+        if layer is None:
+            raise KeyError(f"no cache state for layer {layer_idx}")
+        n = layer.seq_len
+        return (layer.k_packed[:, :, :n], layer.k_scales[:, :, :n],
+                layer.v_packed[:, :, :n], layer.v_scales[:, :, :n])
+
+    def _dequantized(self, layer_idx: int, out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        kp, ks, vp, vs = self.get_quantized(layer_idx)
+        d_head = ks.shape[-1] * self.group_size
+        k = ops.dequantize(kp, ks, self.group_size, d_head, out_dtype)
+        v = ops.dequantize(vp, vs, self.group_size, d_head, out_dtype)
+        return k, v
+
+    def nbytes(self) -> int:
+        """Bytes of packed codes + scales for the stored tokens of all layers
+        (same accounting as the reference, models/llama3/kv_cache.py:158-166)."""
+        total = 0
+        for idx in self._layers:
+            for t in self.get_quantized(idx):
+                total += t.element_size() * t.numel()
+        return total
+
+    def capacity_nbytes(self) -> int:
+        """Bytes actually reserved on the device (capacity buffers)."""
+        total = 0
+        for layer in self._layers.values():
+            for t in (layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales):
+                total += t.element_size() * t.numel()
+        return total

@@ -1,0 +1,384 @@
+"""Device operators of the INT4 KV path, on top of the C ABI.
+
+Everything here works on GPU tensors and enqueues HIP kernels on the current
+stream. The model-family front-ends (``kvint4.llama3``, ``kvint4.gpt2``) add the
+reference's argument contracts and dtype policies on top.
+
+Layouts (bit-identical to the reference's, ``kernels/llama3/quantize.py:7-14``):
+  x       [..., d]                        bf16 / fp16 / fp32
+  packed  [..., ceil(d/G) * ceil(G/2)]    uint8, element 2i -> low nibble of byte i
+  scales  [..., ceil(d/G)]                scale dtype (per family policy)
+"""
+
+from __future__ import annotations
+
+import math
+import threading
+
+import torch
+import torch.nn.functional as F
+
+from . import _native as nat
+
+SUPPORTED_FLOATS = (torch.bfloat16, torch.float16, torch.float32)
+
+# Query rows (GQA group x query length) above which a multi-token query is
+# routed to dequantize + dense SDPA instead of the decode kernel.
+MAX_FUSED_ROWS = 64
+
+
+def packed_width(d: int, group_size: int) -> int:
+    return math.ceil(d / group_size) * ((group_size + 1) // 2)
+
+
+def num_groups(d: int, group_size: int) -> int:
+    return math.ceil(d / group_size)
+
+
+def _as_bhs(t: torch.Tensor) -> tuple[torch.Tensor, tuple[int, int, int], tuple[int, int, int]]:
+    """View the leading dims of `t` as (B, H, S): returns (tensor, sizes, strides).
+
+    Up to three leading dims are used as they are; more are collapsed with
+    `reshape` (a copy only if the strides cannot be merged).
+    """
+    lead = t.dim() - 1
+    if lead > 3:
+        t = t.reshape(-1, t.shape[-1])
+        lead = 1
+    sizes = [1] * (3 - lead) + list(t.shape[:-1])
+    strides = [0] * (3 - lead) + list(t.stride()[:-1])
+    return t, tuple(sizes), tuple(strides)
+
+
+def _check_cuda(*ts: torch.Tensor, what: str) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError(f"{what} expects GPU tensors (got a tensor on {t.device})")
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize
+
+
+def quantize_into(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    write_pos: int | torch.Tensor = 0,
+) -> None:
+    """Quantize x [B, H, S, D] and write the rows at positions pos_b + s of the
+    cache tensors packed [B, H, S_cap, W] / scales [B, H, S_cap, n_groups].
+
+    `write_pos` is an int (same position for every batch row) or a device int32
+    tensor [B] of per-sequence positions.
+    """
+    _check_cuda(x, packed, scales, what="quantize_into")
+    if x.dim() != 4 or packed.dim() != 4 or scales.dim() != 4:
+        raise ValueError("quantize_into expects 4D x, packed and scales")
+    B, H, S, D = x.shape
+    if packed.shape[:2] != (B, H) or scales.shape[:2] != (B, H):
+        raise ValueError("cache leading dims must match x [B, H, ...]")
+    if packed.shape[-1] < packed_width(D, group_size) or scales.shape[-1] < num_groups(D, group_size):
+        raise ValueError("cache last dims are too small for this head dim / group size")
+    if packed.stride(-1) != 1 or scales.stride(-1) != 1:
+        raise ValueError("cache last dims must be contiguous")
+    if packed.dtype != torch.uint8 or scales.dtype not in SUPPORTED_FLOATS:
+        raise ValueError("cache dtypes must be uint8 codes and float scales")
+    wp_ptr, wp0 = None, 0
+    if isinstance(write_pos, torch.Tensor):
+        if write_pos.dtype != torch.int32 or write_pos.numel() != B or not write_pos.is_cuda:
+            raise ValueError("write_pos must be a device int32 tensor of shape [B]")
+        write_pos = write_pos.contiguous()
+        wp_ptr = write_pos.data_ptr()
+    else:
+        wp0 = int(write_pos)
+        if wp0 < 0 or wp0 + S > packed.shape[2] or wp0 + S > scales.shape[2]:
+            raise ValueError("write position out of the cache's range")
+    lib = nat.lib()
+    with nat.device_of(x):
+        rc = lib.kvq_quantize(
+            x.data_ptr(), nat.DTYPE_CODE[x.dtype], nat.i64_array(x.stride()),
+            B, H, S, D, group_size,
+            packed.data_ptr(), nat.i64_array(packed.stride()[:3]),
+            scales.data_ptr(), nat.DTYPE_CODE[scales.dtype], nat.i64_array(scales.stride()[:3]),
+            wp_ptr, wp0, nat.stream_handle(x.device),
+        )
+    nat.check(rc, "kvq_quantize")
+
+
+def quantize(x: torch.Tensor, group_size: int, scale_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fresh (packed, scales) for x [..., d]; scales stored in `scale_dtype`."""
+    _check_cuda(x, what="quantize_int4")
+    lead_shape = x.shape[:-1]
+    d = x.shape[-1]
+    w, ng = packed_width(d, group_size), num_groups(d, group_size)
+    packed = torch.empty((*lead_shape, w), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((*lead_shape, ng), dtype=scale_dtype, device=x.device)
+    if x.numel() == 0 or ng == 0:
+        return packed, scales
+    xv, sizes, strides = _as_bhs(x)
+    pv = packed.reshape(*sizes, w)
+    sv = scales.reshape(*sizes, ng)
+    lib = nat.lib()
+    with nat.device_of(x):
+        rc = lib.kvq_quantize(
+            xv.data_ptr(), nat.DTYPE_CODE[x.dtype], nat.i64_array((*strides, xv.stride(-1))),
+            sizes[0], sizes[1], sizes[2], d, group_size,
+            pv.data_ptr(), nat.i64_array(pv.stride()[:3]),
+            sv.data_ptr(), nat.DTYPE_CODE[scale_dtype], nat.i64_array(sv.stride()[:3]),
+            None, 0, nat.stream_handle(x.device),
+        )
+    nat.check(rc, "kvq_quantize")
+    return packed, scales
+
+
+def dequantize(
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    d_out: int,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """(nibble - 8) * fp32(scale) -> out_dtype, first `d_out` columns."""
+    _check_cuda(packed, scales, what="dequantize_int4")
+    ng = scales.shape[-1]
+    width = packed.shape[-1]
+    if width * 2 < ng * group_size and ng > 0:
+        raise ValueError("packed has insufficient width for the provided group_size")
+    d_out = min(int(d_out), ng * group_size)
+    lead_shape = packed.shape[:-1]
+    out = torch.empty((*lead_shape, d_out), dtype=out_dtype, device=packed.device)
+    if out.numel() == 0:
+        return out
+    if packed.stride(-1) != 1:
+        packed = packed.contiguous()
+    if scales.stride(-1) != 1:
+        scales = scales.contiguous()
+    pv, sizes, pstr = _as_bhs(packed)
+    sv, ssz, sstr = _as_bhs(scales)
+    if ssz != sizes:
+        sv = scales.reshape(*sizes, ng)
+        sstr = sv.stride()[:3]
+    ov = out.reshape(*sizes, d_out)
+    lib = nat.lib()
+    with nat.device_of(packed):
+        rc = lib.kvq_dequantize(
+            pv.data_ptr(), nat.i64_array(pstr),
+            sv.data_ptr(), nat.DTYPE_CODE[scales.dtype], nat.i64_array(sstr),
+            sizes[0], sizes[1], sizes[2], group_size, ng,
+            ov.data_ptr(), nat.DTYPE_CODE[out_dtype], nat.i64_array(ov.stride()), d_out,
+            nat.stream_handle(packed.device),
+        )
+    nat.check(rc, "kvq_dequantize")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# decode attention
+
+
+class _Workspaces:
+    """Zero-initialised split-K workspaces, one per (device, stream).
+
+    The kernel returns its counters to zero, so a workspace is reused across
+    calls issued on the same stream (which are ordered).
+    """
+
+    def __init__(self) -> None:
+        self._lock = threading.Lock()
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 20)
+                if buf is not None:
+                    size = max(size, 2 * buf.numel())
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_workspaces = _Workspaces()
+_cu_count: dict[int, int] = {}
+
+
+def _num_cus(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _cu_count.get(idx)
+    if n is None:
+        n = torch.cuda.get_device_properties(idx).multi_processor_count
+        _cu_count[idx] = n
+    return n
+
+
+def fused_decode_attention(
+    q: torch.Tensor,
+    k_packed: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_packed: torch.Tensor,
+    v_scales: torch.Tensor,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    is_causal: bool,
+    sm_scale: float,
+    seq_lens: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Launch the fused split-K decode kernel; raises KVQUnsupported for shapes
+    it does not handle. q [B, Hq, Sq, D]; K/V codes [B, Hkv, Sk, W] (strided views
+    of a larger cache are fine as long as the last dim is contiguous)."""
+    B, Hq, Sq, D = q.shape
+    Sk = k_packed.shape[2]
+    if out is None:
+        out = torch.empty_like(q)
+    if k_packed.stride(-1) != 1 or v_packed.stride(-1) != 1:
+        raise nat.KVQUnsupported("packed K/V last dim must be contiguous")
+    if k_scales.stride(-1) != 1:
+        k_scales = k_scales.contiguous()
+    if v_scales.stride(-1) != 1:
+        v_scales = v_scales.contiguous()
+    if v_scales.dtype != k_scales.dtype:
+        v_scales = v_scales.to(k_scales.dtype)
+    sl_ptr = None
+    if seq_lens is not None:
+        if seq_lens.dtype != torch.int32 or not seq_lens.is_cuda or seq_lens.numel() != B:
+            raise ValueError("seq_lens must be a device int32 tensor of shape [B]")
+        seq_lens = seq_lens.contiguous()
+        sl_ptr = seq_lens.data_ptr()
+    lib = nat.lib()
+    qd = nat.DTYPE_CODE[q.dtype]
+    n_split = lib.kvq_decode_attn_num_splits(B, Hq, n_kv_heads, Sq, D, Sk, qd, _num_cus(q.device))
+    if n_split < 0:
+        nat.check(int(n_split), "kvq_decode_attn_num_splits")
+    ws_bytes = lib.kvq_decode_attn_workspace_bytes(B, Hq, n_kv_heads, Sq, D, qd, n_split)
+    if ws_bytes < 0:
+        nat.check(int(ws_bytes), "kvq_decode_attn_workspace_bytes")
+    with nat.device_of(q):
+        stream = nat.stream_handle(q.device)
+        ws_ptr, ws_len = None, 0
+        if ws_bytes > 0:
+            ws = _workspaces.get(q.device, stream, ws_bytes)
+            ws_ptr, ws_len = ws.data_ptr(), ws.numel()
+        rc = lib.kvq_decode_attn(
+            q.data_ptr(), qd, nat.i64_array(q.stride()),
+            k_packed.data_ptr(), nat.i64_array(k_packed.stride()[:3]),
+            k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:3]),
+            v_packed.data_ptr(), nat.i64_array(v_packed.stride()[:3]),
+            v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:3]),
+            nat.DTYPE_CODE[k_scales.dtype],
+            out.data_ptr(), nat.i64_array(out.stride()),
+            B, Hq, n_kv_heads, Sq, D, group_size, Sk,
+            sl_ptr, 1 if is_causal else 0, float(sm_scale),
+            n_split, ws_ptr, ws_len, stream,
+        )
+    nat.check(rc, "kvq_decode_attn")
+    return out
+
+
+def _sdpa_dense(q, k, v, *, is_causal: bool, sm_scale: float, attn_mask=None) -> torch.Tensor:
+    """Dense attention on already-dequantized, GQA-expanded K/V.
+
+    bf16/fp16 run on the fused flash / memory-efficient SDPA backends only (the
+    math backend would issue batched GEMMs on transposed half-precision views);
+    fp32 uses the math backend.
+    """
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    if q.dtype in (torch.bfloat16, torch.float16) and attn_mask is None:
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return F.scaled_dot_product_attention(q, k, v, is_causal=is_causal, scale=sm_scale)
+        except RuntimeError:
+            pass
+    qf, kf, vf = q.float(), k.float(), v.float()
+    with sdpa_kernel([SDPBackend.MATH]):
+        o = F.scaled_dot_product_attention(
+            qf, kf, vf, attn_mask=attn_mask, is_causal=is_causal and attn_mask is None, scale=sm_scale
+        )
+    return o.to(q.dtype)
+
+
+def dense_attention_over_quantized(
+    q: torch.Tensor,
+    k_packed: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_packed: torch.Tensor,
+    v_scales: torch.Tensor,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    is_causal: bool,
+    sm_scale: float,
+    seq_lens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Long query blocks (prefill) and shapes outside the fused kernel: HIP
+    dequantize of the INT4 cache, then dense SDPA. Causal masking is aligned to
+    the bottom-right corner (query i sees keys j <= Sk - Sq + i), as in the
+    reference kernel (kernels/llama3/attention_quant.py:91-97,123)."""
+    B, Hq, Sq, D = q.shape
+    Sk = k_packed.shape[2]
+    deq_dtype = q.dtype
+    k = dequantize(k_packed, k_scales, group_size, D, deq_dtype)
+    v = dequantize(v_packed, v_scales, group_size, D, deq_dtype)
+    ratio = Hq // n_kv_heads
+    if ratio > 1:
+        k = k.repeat_interleave(ratio, dim=1)
+        v = v.repeat_interleave(ratio, dim=1)
+    mask = None
+    if seq_lens is not None or (is_causal and Sq != Sk):
+        jj = torch.arange(Sk, device=q.device)
+        ii = torch.arange(Sq, device=q.device)
+        lens = (seq_lens.to(torch.int64) if seq_lens is not None
+                else torch.full((B,), Sk, dtype=torch.int64, device=q.device))
+        allowed = jj[None, None, :] < lens[:, None, None]  # [B, 1, Sk]
+        if is_causal:
+            allowed = allowed & (jj[None, None, :] <= (lens[:, None, None] - Sq + ii[None, :, None]))
+        mask = allowed[:, None, :, :]  # [B, 1, Sq, Sk]
+        out = _sdpa_dense(q, k, v, is_causal=False, sm_scale=sm_scale, attn_mask=mask)
+        # rows with no admissible key: zeros (the fused kernel's convention)
+        empty = ~allowed.any(dim=-1)  # [B, Sq]
+        if bool(empty.any()):
+            out = out.masked_fill(empty[:, None, :, None], 0)
+        return out
+    return _sdpa_dense(q, k, v, is_causal=is_causal, sm_scale=sm_scale)
+
+
+def attention_over_quantized(
+    q: torch.Tensor,
+    k_packed: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_packed: torch.Tensor,
+    v_scales: torch.Tensor,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    is_causal: bool,
+    sm_scale: float,
+    seq_lens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Route to the fused decode kernel when the query block is short (decode,
+    small speculative blocks) or when bottom-right causal masking is needed;
+    long blocks go to dequantize + dense SDPA."""
+    B, Hq, Sq, D = q.shape
+    Sk = k_packed.shape[2]
+    rows = (Hq // n_kv_heads) * Sq
+    use_fused = rows <= MAX_FUSED_ROWS or (is_causal and Sq != Sk)
+    if use_fused:
+        try:
+            return fused_decode_attention(
+                q, k_packed, k_scales, v_packed, v_scales,
+                n_kv_heads=n_kv_heads, group_size=group_size, is_causal=is_causal,
+                sm_scale=sm_scale, seq_lens=seq_lens,
+            )
+        except nat.KVQUnsupported:
+            pass
+    return dense_attention_over_quantized(
+        q, k_packed, k_scales, v_packed, v_scales,
+        n_kv_heads=n_kv_heads, group_size=group_size, is_causal=is_causal,
+        sm_scale=sm_scale, seq_lens=seq_lens,
+    )

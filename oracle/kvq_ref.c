@@ -1,0 +1,218 @@
+/*
+ * kvq_ref.c — C restatement of the reference's CPU path for the INT4 KV hot
+ * path. TEST INFRASTRUCTURE ONLY: used by tests/ as a second, independent
+ * checker (cross-validated against oracle/kvq_oracle.py) and timed by
+ * bench.py's cpu_baseline leg. The product library never links it.
+ *
+ *   kvqref_quantize    kernels/llama3/quantize.py:126-148 (_quantize_int4_torch)
+ *   kvqref_dequantize  kernels/llama3/quantize.py:210-234 (_dequantize_int4_torch)
+ *   kvqref_decode_attn dequantize + softmax(q k^T * scale) v, the reference's
+ *                      attention oracle (tests/llama3/test_attention_quant_gqa.py:
+ *                      21-40: dequantize, repeat_interleave over the GQA group,
+ *                      SDPA) with the kernel's bottom-right causal alignment
+ *                      (kernels/llama3/attention_quant.py:91-97,123).
+ *
+ * Values are passed as float32 (a bf16/fp16 tensor as the float32 array of its
+ * values); scale_dtype / out_dtype select round-to-nearest-even narrowing:
+ * 0 = bf16, 1 = fp16, 2 = fp32. Attention runs in fp32 with a split over the
+ * key axis (partial max / sum / output per split, merged exactly as a
+ * log-sum-exp), parallelised with OpenMP over (batch, kv head, split).
+ */
+#include <immintrin.h> /* F16C: _cvtss_sh / _cvtsh_ss (part of x86-64-v3) */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static float round_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    u = 0x7fc00000u;
+  } else {
+    u = (uint32_t)(((uint64_t)u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+  }
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static float round_f16(float f) { return _cvtsh_ss(_cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT)); }
+
+static float round_to(float f, int dt) {
+  if (dt == 0) return round_bf16(f);
+  if (dt == 1) return round_f16(f);
+  return f;
+}
+
+int kvqref_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void kvqref_quantize(const float* x, int64_t rows, int64_t d, int64_t G, int scale_dtype,
+                     uint8_t* packed, float* scales) {
+  const int64_t ng = (d + G - 1) / G;
+  const int64_t bpg = (G + 1) / 2;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * d;
+    uint8_t* pr = packed + r * ng * bpg;
+    for (int64_t g = 0; g < ng; ++g) {
+      float amax = 0.0f;
+      for (int64_t k = 0; k < G; ++k) {
+        const int64_t c = g * G + k;
+        const float v = c < d ? fabsf(xr[c]) : 0.0f;
+        if (v > amax) amax = v;
+      }
+      const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+      for (int64_t j = 0; j < bpg; ++j) {
+        unsigned nib[2];
+        for (int e = 0; e < 2; ++e) {
+          const int64_t k = 2 * j + e;
+          if (k >= G) {
+            nib[e] = 0;
+            continue;
+          }
+          const int64_t c = g * G + k;
+          const float v = c < d ? xr[c] : 0.0f;
+          float q = nearbyintf(v / scale); /* default FE_TONEAREST: half to even */
+          if (q < -8.0f) q = -8.0f;
+          if (q > 7.0f) q = 7.0f;
+          nib[e] = (unsigned)((int)q + 8);
+        }
+        pr[g * bpg + j] = (uint8_t)(nib[0] | (nib[1] << 4));
+      }
+      scales[r * ng + g] = round_to(scale, scale_dtype);
+    }
+  }
+}
+
+void kvqref_dequantize(const uint8_t* packed, const float* scales, int64_t rows, int64_t ng,
+                       int64_t G, int64_t d_out, int out_dtype, float* out) {
+  const int64_t bpg = (G + 1) / 2;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < d_out; ++c) {
+      const int64_t g = c / G, k = c % G;
+      const uint8_t byte = packed[r * ng * bpg + g * bpg + k / 2];
+      const int nib = (k & 1) ? (byte >> 4) : (byte & 15);
+      out[r * d_out + c] = round_to((float)(nib - 8) * scales[r * ng + g], out_dtype);
+    }
+  }
+}
+
+/* Dequantize one packed row of D elements (group size G) into dst. */
+static void deq_row(const uint8_t* p, const float* s, int64_t D, int64_t G, float* dst) {
+  const int64_t bpg = (G + 1) / 2;
+  for (int64_t c = 0; c < D; ++c) {
+    const int64_t g = c / G, k = c % G;
+    const uint8_t byte = p[g * bpg + k / 2];
+    const int nib = (k & 1) ? (byte >> 4) : (byte & 15);
+    dst[c] = (float)(nib - 8) * s[g];
+  }
+}
+
+int kvqref_decode_attn(const float* q, const uint8_t* kp, const float* ks, const uint8_t* vp,
+                       const float* vs, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                       int64_t Sk, int64_t D, int64_t G, const int32_t* seq_lens, int causal,
+                       float scale, float* out, int nthreads) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq <= 0 || D <= 0 || G <= 0 || Hq % Hkv) return -1;
+  const int64_t ratio = Hq / Hkv, rows = ratio * Sq;
+  const int64_t ng = (D + G - 1) / G, W = ng * ((G + 1) / 2);
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#else
+  nthreads = 1;
+#endif
+  int64_t n_split = (2 * (int64_t)nthreads + B * Hkv - 1) / (B * Hkv);
+  if (n_split < 1) n_split = 1;
+  int64_t split_len = (Sk + n_split - 1) / n_split;
+  if (split_len < 64) split_len = 64;
+  n_split = Sk > 0 ? (Sk + split_len - 1) / split_len : 1;
+  const int64_t tasks = B * Hkv * n_split;
+  /* partials: [tasks][rows] (m, l) and [tasks][rows][D] o */
+  float* pm = (float*)malloc(sizeof(float) * tasks * rows);
+  float* pl = (float*)malloc(sizeof(float) * tasks * rows);
+  float* po = (float*)malloc(sizeof(float) * tasks * rows * D);
+  if (!pm || !pl || !po) {
+    free(pm); free(pl); free(po);
+    return -2;
+  }
+#pragma omp parallel for schedule(dynamic) num_threads(nthreads)
+  for (int64_t t = 0; t < tasks; ++t) {
+    const int64_t sp = t % n_split, bh = t / n_split, h = bh % Hkv, b = bh / Hkv;
+    int64_t L = Sk;
+    if (seq_lens) L = seq_lens[b] < 0 ? 0 : (seq_lens[b] < Sk ? seq_lens[b] : Sk);
+    const int64_t j0 = sp * split_len, j1 = (j0 + split_len < L) ? j0 + split_len : L;
+    const int64_t n = j1 > j0 ? j1 - j0 : 0;
+    float* kbuf = (float*)malloc(sizeof(float) * (n > 0 ? n : 1) * D);
+    float* vbuf = (float*)malloc(sizeof(float) * (n > 0 ? n : 1) * D);
+    float* sc = (float*)malloc(sizeof(float) * (n > 0 ? n : 1));
+    for (int64_t j = 0; j < n; ++j) {
+      const int64_t row = (b * Hkv + h) * Sk + j0 + j;
+      deq_row(kp + row * W, ks + row * ng, D, G, kbuf + j * D);
+      deq_row(vp + row * W, vs + row * ng, D, G, vbuf + j * D);
+    }
+    for (int64_t rr = 0; rr < rows; ++rr) {
+      const int64_t hq = h * ratio + rr / Sq, qi = rr % Sq;
+      const float* qv = q + ((b * Hq + hq) * Sq + qi) * D;
+      const int64_t lim = causal ? (L - Sq + qi + 1) : L; /* keys j < lim */
+      float m = -INFINITY, l = 0.0f;
+      float* o = po + (t * rows + rr) * D;
+      for (int64_t c = 0; c < D; ++c) o[c] = 0.0f;
+      for (int64_t j = 0; j < n; ++j) {
+        if (j0 + j >= lim) { sc[j] = -INFINITY; continue; }
+        float acc = 0.0f;
+        const float* kr = kbuf + j * D;
+        for (int64_t c = 0; c < D; ++c) acc += qv[c] * kr[c];
+        sc[j] = acc * scale;
+        if (sc[j] > m) m = sc[j];
+      }
+      if (m != -INFINITY) {
+        for (int64_t j = 0; j < n; ++j) {
+          if (sc[j] == -INFINITY) continue;
+          const float p = expf(sc[j] - m);
+          l += p;
+          const float* vr = vbuf + j * D;
+          for (int64_t c = 0; c < D; ++c) o[c] += p * vr[c];
+        }
+      }
+      pm[t * rows + rr] = m;
+      pl[t * rows + rr] = l;
+    }
+    free(kbuf); free(vbuf); free(sc);
+  }
+  /* merge the splits */
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+  for (int64_t u = 0; u < B * Hkv * rows; ++u) {
+    const int64_t rr = u % rows, bh = u / rows, h = bh % Hkv, b = bh / Hkv;
+    const int64_t hq = h * ratio + rr / Sq, qi = rr % Sq;
+    float M = -INFINITY;
+    for (int64_t sp = 0; sp < n_split; ++sp) {
+      const float m = pm[(bh * n_split + sp) * rows + rr];
+      if (m > M) M = m;
+    }
+    float* dst = out + ((b * Hq + hq) * Sq + qi) * D;
+    for (int64_t c = 0; c < D; ++c) dst[c] = 0.0f;
+    if (M == -INFINITY) continue;
+    float Ls = 0.0f;
+    for (int64_t sp = 0; sp < n_split; ++sp) {
+      const int64_t t = bh * n_split + sp;
+      const float m = pm[t * rows + rr];
+      if (m == -INFINITY) continue;
+      const float f = expf(m - M);
+      Ls += pl[t * rows + rr] * f;
+      const float* o = po + (t * rows + rr) * D;
+      for (int64_t c = 0; c < D; ++c) dst[c] += o[c] * f;
+    }
+    for (int64_t c = 0; c < D; ++c) dst[c] /= Ls;
+  }
+  free(pm); free(pl); free(po);
+  return 0;
+}

@@ -1,0 +1,92 @@
+"""The C-ABI library: it loads, exports every symbol include/kvint4.h declares,
+and its host-only entry points (planning, argument validation) behave. No
+kernel is launched here (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from kvint4 import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols() -> set[str]:
+    text = open(os.path.join(ROOT, "include", "kvint4.h")).read()
+    return set(re.findall(r"^\s*(?:int64_t|int|const char\*)\s+(kvq_\w+)\s*\(", text, re.M))
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == set(nat.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.lib()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_version_and_error_slot():
+    lib = nat.lib()
+    assert lib.kvq_version() >= 100
+    assert isinstance(nat.last_error(), str)
+
+
+def test_num_splits_planning():
+    lib = nat.lib()
+    # Llama-3.1-8B decode at 16K on 256 CUs: 8 KV heads x 32 splits
+    assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 16384, nat.KVQ_BF16, 256) == 32
+    # never more splits than 4-wave tiles of tokens
+    assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 100, nat.KVQ_BF16, 256) == 2
+    # plenty of units already -> one split
+    assert lib.kvq_decode_attn_num_splits(16, 25, 25, 1, 64, 1024, nat.KVQ_F16, 256) == 1
+    assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 96, 1024, nat.KVQ_BF16, 256) == nat.KVQ_EUNSUP
+    assert lib.kvq_decode_attn_num_splits(1, 30, 8, 1, 128, 1024, nat.KVQ_BF16, 256) == nat.KVQ_EINVAL
+
+
+def test_workspace_bytes():
+    lib = nat.lib()
+    assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, nat.KVQ_BF16, 1) == 0
+    ws = lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, nat.KVQ_BF16, 32)
+    # 8 units x 32 splits x 4 rows x (128 + 2) floats, plus an aligned counter block
+    assert ws >= 8 * 32 * 4 * 130 * 4 and ws < 8 * 32 * 4 * 130 * 4 + 1024
+    assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, 7, 4) == nat.KVQ_EINVAL
+
+
+def test_invalid_arguments_rejected_before_any_launch():
+    lib = nat.lib()
+    s4 = nat.i64_array([0, 0, 0, 1])
+    s3 = nat.i64_array([0, 0, 0])
+    rc = lib.kvq_quantize(None, nat.KVQ_BF16, s4, 1, 1, 1, 128, 0, None, s3, None, nat.KVQ_BF16, s3,
+                          None, 0, None)
+    assert rc == nat.KVQ_EINVAL and "group_size" in nat.last_error()
+    rc = lib.kvq_quantize(None, 9, s4, 1, 1, 1, 128, 32, None, s3, None, nat.KVQ_BF16, s3, None, 0, None)
+    assert rc == nat.KVQ_EINVAL and "dtype" in nat.last_error()
+    rc = lib.kvq_quantize(None, nat.KVQ_BF16, s4, 1, 1, 1, 128, 32, None, s3, None, nat.KVQ_BF16, s3,
+                          None, 0, None)
+    assert rc == nat.KVQ_EINVAL and "null" in nat.last_error()
+    rc = lib.kvq_dequantize(None, s3, None, nat.KVQ_BF16, s3, 1, 1, 1, 32, 4, None, nat.KVQ_BF16, s4,
+                            200, None)
+    assert rc == nat.KVQ_EINVAL and "d_out" in nat.last_error()
+    rc = lib.kvq_decode_attn(None, nat.KVQ_BF16, s4, None, s3, None, s3, None, s3, None, s3,
+                             nat.KVQ_BF16, None, s4, 1, 6, 4, 1, 128, 32, 16, None, 0, 1.0, 1,
+                             None, 0, None)
+    assert rc == nat.KVQ_EINVAL and "multiple" in nat.last_error()
+    rc = lib.kvq_decode_attn(None, nat.KVQ_BF16, s4, None, s3, None, s3, None, s3, None, s3,
+                             nat.KVQ_BF16, None, s4, 1, 8, 4, 1, 96, 32, 16, None, 0, 1.0, 1,
+                             None, 0, None)
+    assert rc == nat.KVQ_EUNSUP
+
+
+def test_check_maps_status_to_exceptions():
+    with pytest.raises(ValueError):
+        nat.check(nat.KVQ_EINVAL, "x")
+    with pytest.raises(nat.KVQUnsupported):
+        nat.check(nat.KVQ_EUNSUP, "x")
+    with pytest.raises(RuntimeError):
+        nat.check(nat.KVQ_EHIP, "x")

@@ -1,0 +1,170 @@
+"""GPU: QuantizedKVCache storage and the HF attention glue.
+
+Cache: chunked appends (and capacity growth) equal one-shot quantization of
+the concatenation bit for bit — the reference's append is quantize + torch.cat
+(models/llama3/kv_cache.py:76-102); views, nbytes, the transformers 5.x cache
+protocol, ragged appends.
+
+Model glue (tests/llama3/test_llama3_quant_decode.py:21-122,
+tests/llama3/test_llama3_generate_parity.py:52-74): a tiny random-init Llama
+(and GPT-2) swapped to the INT4 path on the GPU vs the stock model with a
+DynamicCache on the CPU (bf16 batched products stay off the GPU), with the
+reference's own bars: prefill last-logit max-abs < 1.0 and same argmax, 8
+decode steps < 2.0, greedy prefix agreement >= 4 of 16.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from transformers import GPT2Config, GPT2LMHeadModel, LlamaConfig, LlamaForCausalLM
+from transformers.cache_utils import DynamicCache
+
+from kvint4.gpt2.gpt2_quant import replace_gpt2_attention_with_quantized
+from kvint4.gpt2.kv_cache import QuantizedKVCache as GPT2Cache
+from kvint4.llama3.kv_cache import QuantizedKVCache
+from kvint4.llama3.llama3_quant import LlamaAttentionQuantized, replace_llama_attention_with_quantized
+from oracle import kvq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def test_chunked_append_equals_one_shot_and_growth():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 4, 700, 128, generator=g).to(torch.bfloat16)
+    y = torch.randn(2, 4, 700, 128, generator=g).to(torch.bfloat16)
+    cache = QuantizedKVCache(group_size=32)
+    bounds = [0, 37, 38, 300, 301, 302, 700]  # first allocation is 256 + 37 rounded; forces growth
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        cache.append(x[:, :, a:b].to(DEV), y[:, :, a:b].to(DEV), 3)
+    assert cache.get_seq_length(3) == 700 and cache.get_seq_length(0) == 0
+    kp, ks, vp, vs = cache.get_quantized(3)
+    assert kp.shape == (2, 4, 700, 64) and ks.shape == (2, 4, 700, 4) and ks.dtype == torch.bfloat16
+    okp, oks = O.quantize_int4(x.float().numpy(), 32, "bf16")
+    ovp, ovs = O.quantize_int4(y.float().numpy(), 32, "bf16")
+    assert np.array_equal(kp.cpu().numpy(), okp) and np.array_equal(vp.cpu().numpy(), ovp)
+    assert np.array_equal(ks.float().cpu().numpy(), oks) and np.array_equal(vs.float().cpu().numpy(), ovs)
+    assert cache.nbytes() == 2 * (2 * 4 * 700 * 64) + 2 * (2 * 4 * 700 * 4 * 2)
+    assert cache.capacity_nbytes() >= cache.nbytes()
+    k_deq, v_deq = cache.get_dequantized(3, out_dtype=torch.float32)
+    assert np.array_equal(k_deq.cpu().numpy(), O.dequantize_int4(okp, oks, 32, 128, "f32"))
+
+
+def test_protocol_and_update_path():
+    cache = QuantizedKVCache()
+    k = torch.randn(1, 2, 5, 64, device=DEV, dtype=torch.float32)
+    kd, vd = cache.update(k, k, 0)
+    assert kd.dtype == torch.float32 and kd.shape == (1, 2, 5, 64)
+    assert cache.get_mask_sizes(3, 0) == (8, 0)
+    assert cache.get_mask_sizes(torch.arange(3), 0) == (8, 0)
+    assert cache.get_query_offset(0) == 5
+    assert cache.is_sliding == [False] and cache.is_initialized and len(cache) == 1
+    assert cache.get_max_cache_shape() == -1
+    gc = GPT2Cache()
+    kd, _ = gc.update(k, k, 0)
+    assert kd.dtype == torch.float16 and gc.get_max_cache_shape() is None
+    cache.reset()
+    assert not cache.is_initialized
+
+
+def test_ragged_append_positions():
+    cache = GPT2Cache(group_size=32)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 2, 40, 64, generator=g).half()
+    lens = torch.tensor([5, 40, 17])
+    cache.load_ragged(x.to(DEV), x.to(DEV), 0, lens)
+    new = torch.randn(3, 2, 1, 64, generator=g).half()
+    cache.append(new.to(DEV), new.to(DEV), 0)
+    assert cache.get_seq_lens(0).tolist() == [6, 41, 18]
+    kp, ks, _, _ = cache.get_quantized(0)
+    want_p, _ = O.quantize_int4(new.float().numpy(), 32, "f16")
+    for b, p in enumerate([5, 40, 17]):
+        assert np.array_equal(kp[b, :, p].cpu().numpy(), want_p[b, :, 0])
+
+
+def _tiny_llama(dtype=torch.bfloat16):
+    cfg = LlamaConfig(vocab_size=256, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=64,
+                      max_position_embeddings=512, rms_norm_eps=1e-5, tie_word_embeddings=False,
+                      attention_bias=False, mlp_bias=False)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).to(dtype=dtype).eval()
+
+
+def test_llama_prefill_decode_matches_reference():
+    ref = _tiny_llama()                      # stock model, DynamicCache, CPU
+    quant = _tiny_llama()
+    quant.load_state_dict(ref.state_dict())
+    replace_llama_attention_with_quantized(quant, group_size=32)
+    quant = quant.to(DEV)
+    assert all(isinstance(l.self_attn, LlamaAttentionQuantized) for l in quant.model.layers)
+    torch.manual_seed(123)
+    prompt = torch.randint(0, 256, (1, 32))
+    with torch.no_grad():
+        cache_ref, cache_q = DynamicCache(), QuantizedKVCache(group_size=32)
+        out_r = ref(input_ids=prompt, past_key_values=cache_ref, use_cache=True)
+        out_q = quant(input_ids=prompt.to(DEV), past_key_values=cache_q, use_cache=True)
+        lr, lq = out_r.logits[:, -1].float(), out_q.logits[:, -1].float().cpu()
+        assert (lr - lq).abs().max().item() < 1.0
+        assert lr.argmax(-1).item() == lq.argmax(-1).item()
+        for step in range(8):
+            nid = torch.randint(0, 256, (1, 1))
+            out_r = ref(input_ids=nid, past_key_values=cache_ref, use_cache=True)
+            out_q = quant(input_ids=nid.to(DEV), past_key_values=cache_q, use_cache=True)
+            d = (out_r.logits[:, -1].float() - out_q.logits[:, -1].float().cpu()).abs().max().item()
+            assert d < 2.0, f"decode step {step}: {d}"
+    assert cache_q.get_seq_length(0) == 40
+    seq = 40
+    assert cache_q.nbytes() < (2 * 2 * 1 * 2 * seq * 64 * 2) / 2
+
+
+def test_llama_greedy_prefix_agreement():
+    ref = _tiny_llama()
+    quant = _tiny_llama()
+    quant.load_state_dict(ref.state_dict())
+    replace_llama_attention_with_quantized(quant)
+    quant = quant.to(DEV)
+    torch.manual_seed(321)
+    prompt = torch.randint(0, 256, (1, 24))
+
+    def greedy(model, dev, cache, n):
+        toks = []
+        with torch.no_grad():
+            out = model(input_ids=prompt.to(dev), past_key_values=cache, use_cache=True)
+            nid = out.logits[:, -1].argmax(-1, keepdim=True)
+            toks.append(int(nid.item()))
+            for _ in range(n - 1):
+                out = model(input_ids=nid, past_key_values=cache, use_cache=True)
+                nid = out.logits[:, -1].argmax(-1, keepdim=True)
+                toks.append(int(nid.item()))
+        return toks
+
+    a = greedy(ref, "cpu", DynamicCache(), 16)
+    b = greedy(quant, DEV, QuantizedKVCache(), 16)
+    agree = next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), 16)
+    assert agree >= 4, (a, b)
+
+
+def test_gpt2_random_init_decode_matches_reference():
+    cfg = GPT2Config(n_layer=2, n_head=4, n_embd=128, vocab_size=256, n_positions=256)
+    torch.manual_seed(0)
+    ref = GPT2LMHeadModel(cfg).eval()                       # fp32, CPU, DynamicCache
+    quant = GPT2LMHeadModel(cfg).eval()
+    quant.load_state_dict(ref.state_dict())
+    replace_gpt2_attention_with_quantized(quant)
+    quant = quant.to(DEV)
+    torch.manual_seed(7)
+    prompt = torch.randint(0, 256, (1, 20))
+    with torch.no_grad():
+        cr, cq = DynamicCache(), GPT2Cache()
+        lr = ref(input_ids=prompt, past_key_values=cr, use_cache=True).logits[:, -1]
+        lq = quant(input_ids=prompt.to(DEV), past_key_values=cq, use_cache=True).logits[:, -1].cpu()
+        assert (lr - lq).abs().max().item() < 1.0 and lr.argmax().item() == lq.argmax().item()
+        for _ in range(6):
+            nid = torch.randint(0, 256, (1, 1))
+            lr = ref(input_ids=nid, past_key_values=cr, use_cache=True).logits[:, -1]
+            lq = quant(input_ids=nid.to(DEV), past_key_values=cq, use_cache=True).logits[:, -1].cpu()
+            assert (lr - lq).abs().max().item() < 2.0
+    assert cq.get_seq_length(0) == 26

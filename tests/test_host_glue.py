@@ -1,0 +1,172 @@
+"""Host logic of the cache and the HF glue, on the CPU.
+
+The native ops are replaced, inside this test only, by fakes built on the CPU
+oracle (a fake backend, as the reference's tests mock kernel calls with
+unittest.mock — tests/gpt2/test_gpt2_triton_routing.py:33-37). This checks
+that transformers 5.x drives the cache protocol and the swapped attention
+modules as expected (call counts, routing, shapes, positions) without a GPU.
+The product path itself has no CPU implementation: without the fakes, CPU
+tensors raise ValueError.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from transformers import GPT2Config, GPT2LMHeadModel, LlamaConfig, LlamaForCausalLM
+from transformers.cache_utils import DynamicCache
+
+import kvint4.gpt2.gpt2_quant as g2q
+import kvint4.llama3.llama3_quant as l3q
+from kvint4 import cache_base, ops
+from kvint4.gpt2.kv_cache import QuantizedKVCache as GPT2Cache
+from kvint4.llama3.attention_quant import attention_forward_quant_gqa
+from kvint4.llama3.kv_cache import QuantizedKVCache, _LayerQuantizedKV
+from oracle import kvq_oracle as O
+
+_NP = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+class FakeBackend:
+    def __init__(self):
+        self.calls = {"quantize_into": 0, "attention": 0, "dequantize": 0}
+
+    def quantize_into(self, x, packed, scales, group_size, write_pos=0):
+        self.calls["quantize_into"] += 1
+        p, s = O.quantize_int4(x.float().numpy(), group_size, _NP[scales.dtype])
+        S = x.shape[2]
+        if isinstance(write_pos, torch.Tensor):
+            for b, p0 in enumerate(write_pos.tolist()):
+                packed[b, :, p0:p0 + S] = torch.from_numpy(p[b])
+                scales[b, :, p0:p0 + S] = torch.from_numpy(s[b]).to(scales.dtype)
+        else:
+            packed[:, :, write_pos:write_pos + S] = torch.from_numpy(p)
+            scales[:, :, write_pos:write_pos + S] = torch.from_numpy(s).to(scales.dtype)
+
+    def dequantize(self, packed, scales, group_size, d_out, out_dtype):
+        self.calls["dequantize"] += 1
+        out = O.dequantize_int4(packed.numpy(), scales.float().numpy(), group_size, d_out, _NP[out_dtype])
+        return torch.from_numpy(out).to(out_dtype)
+
+    def attention(self, q, kp, ks, vp, vs, *, n_q_heads, n_kv_heads, group_size=32, is_causal=False,
+                  scale=None, seq_lens=None):
+        self.calls["attention"] += 1
+        out = O.attention_over_quantized(q.float().numpy(), kp.numpy(), ks.float().numpy(), vp.numpy(),
+                                         vs.float().numpy(), group_size=group_size, scale=scale,
+                                         is_causal=is_causal,
+                                         seq_lens=None if seq_lens is None else seq_lens.tolist())
+        return torch.from_numpy(out.astype(np.float32)).to(q.dtype)
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    fb = FakeBackend()
+    monkeypatch.setattr(ops, "quantize_into", fb.quantize_into)
+    monkeypatch.setattr(ops, "dequantize", fb.dequantize)
+    monkeypatch.setattr(l3q, "attention_forward_quant_gqa", fb.attention)
+
+    def gpt2_attn(q, kp, ks, vp, vs, *, group_size=32, is_causal=False, scale=None, seq_lens=None):
+        return fb.attention(q, kp, ks, vp, vs, n_q_heads=q.shape[1], n_kv_heads=q.shape[1],
+                            group_size=group_size, is_causal=is_causal, scale=scale, seq_lens=seq_lens)
+
+    monkeypatch.setattr(g2q, "attention_forward_quant", gpt2_attn)
+    return fb
+
+
+def _tiny_llama():
+    cfg = LlamaConfig(vocab_size=256, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=64,
+                      max_position_embeddings=512, tie_word_embeddings=False)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).eval()
+
+
+def test_llama_glue_routing_and_logits(fake):
+    ref = _tiny_llama()
+    quant = _tiny_llama()
+    quant.load_state_dict(ref.state_dict())
+    l3q.replace_llama_attention_with_quantized(quant, group_size=32)
+    l3q.replace_llama_attention_with_quantized(quant, group_size=64)  # idempotent: only updates G
+    assert all(l.self_attn.quant_group_size == 64 for l in quant.model.layers)
+    l3q.replace_llama_attention_with_quantized(quant, group_size=32)
+    assert quant.model.layers[0].self_attn.q_proj.weight is not None
+    prompt = torch.randint(0, 256, (1, 12), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        cr, cq = DynamicCache(), QuantizedKVCache()
+        lr = ref(input_ids=prompt, past_key_values=cr, use_cache=True).logits[:, -1]
+        lq = quant(input_ids=prompt, past_key_values=cq, use_cache=True).logits[:, -1]
+        assert fake.calls["attention"] == 2 and fake.calls["quantize_into"] == 4
+        assert (lr - lq).abs().max() < 1.0
+        for _ in range(3):
+            nid = torch.randint(0, 256, (1, 1))
+            ref(input_ids=nid, past_key_values=cr, use_cache=True)
+            quant(input_ids=nid, past_key_values=cq, use_cache=True)
+    assert fake.calls["attention"] == 8
+    assert cq.get_seq_length(0) == 15 and cq.get_seq_length(1) == 15
+
+
+def test_llama_masked_input_takes_dequant_path(fake):
+    model = _tiny_llama()
+    l3q.replace_llama_attention_with_quantized(model)
+    ids = torch.randint(0, 256, (2, 6), generator=torch.Generator().manual_seed(2))
+    mask = torch.ones(2, 6, dtype=torch.long)
+    mask[0, :2] = 0  # left padding -> a real mask reaches attention
+    with torch.no_grad():
+        model(input_ids=ids, attention_mask=mask, past_key_values=QuantizedKVCache(), use_cache=True)
+    assert fake.calls["attention"] == 0 and fake.calls["dequantize"] == 4
+
+
+def test_gpt2_glue_routing(fake):
+    cfg = GPT2Config(n_layer=2, n_head=4, n_embd=64, vocab_size=128, n_positions=64)
+    torch.manual_seed(0)
+    ref = GPT2LMHeadModel(cfg).eval()
+    quant = GPT2LMHeadModel(cfg).eval()
+    quant.load_state_dict(ref.state_dict())
+    g2q.replace_gpt2_attention_with_quantized(quant)
+    prompt = torch.randint(0, 128, (1, 9), generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        cr, cq = DynamicCache(), GPT2Cache()
+        lr = ref(input_ids=prompt, past_key_values=cr, use_cache=True).logits[:, -1]
+        lq = quant(input_ids=prompt, past_key_values=cq, use_cache=True).logits[:, -1]
+        assert (lr - lq).abs().max() < 1.0
+        nid = torch.randint(0, 128, (1, 1))
+        ref(input_ids=nid, past_key_values=cr, use_cache=True)
+        quant(input_ids=nid, past_key_values=cq, use_cache=True)
+    assert fake.calls["attention"] == 4
+    assert cq.get_seq_length(1) == 10
+    assert cq.get_quantized(0)[1].dtype == torch.float16
+
+
+def test_cache_storage_accounting_matches_reference():
+    # tests/gpt2/test_kv_cache_metrics.py:26-41
+    cache = GPT2Cache(group_size=32)
+    k_p = torch.zeros(1, 2, 3, 8, dtype=torch.uint8)
+    k_s = torch.zeros(1, 2, 3, 2, dtype=torch.float16)
+    v_p = torch.ones(1, 2, 3, 8, dtype=torch.uint8)
+    v_s = torch.ones(1, 2, 3, 2, dtype=torch.float16)
+    cache._layers[0] = _LayerQuantizedKV(k_packed=k_p, k_scales=k_s, v_packed=v_p, v_scales=v_s, seq_len=3)
+    assert cache.nbytes() == sum(t.element_size() * t.numel() for t in (k_p, k_s, v_p, v_s))
+
+
+def test_cache_protocol_without_kernels():
+    c = QuantizedKVCache()
+    assert c.get_seq_length() == 0 and c.get_query_offset() == 0
+    assert c.get_mask_sizes(4, 0) == (4, 0) and c.get_mask_sizes(torch.tensor(4), 0) == (4, 0)
+    assert c.is_sliding == [] and not c.is_initialized and c.is_compileable is False
+    with pytest.raises(ValueError):
+        QuantizedKVCache(group_size=0)
+    with pytest.raises(KeyError):
+        c.get_quantized(0)
+
+
+def test_cpu_tensors_are_rejected_by_the_product_path():
+    q = torch.randn(1, 8, 1, 128)
+    kp = torch.zeros(1, 2, 4, 64, dtype=torch.uint8)
+    ks = torch.ones(1, 2, 4, 4)
+    with pytest.raises(ValueError, match="CUDA"):
+        attention_forward_quant_gqa(q, kp, ks, kp, ks, n_q_heads=8, n_kv_heads=2)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.quantize(torch.randn(2, 64), 32, torch.float32)
+    with pytest.raises(ValueError):
+        cache_base.QuantizedKVCacheBase(group_size=-1)
