@@ -99,10 +99,13 @@ int kvq_dequantize(const void* packed, const int64_t* packed_strides,
  * Split-K planning for kvq_decode_attn. Pure host arithmetic (no device call):
  * returns the number of sequence splits the fused kernel will use for this
  * shape on a device with `num_cus` compute units (>= 1), or a negative status.
- * `s_max` is the longest sequence (tokens) that will be attended.
+ * `s_max` is the longest sequence (tokens) that will be attended. bf16/fp16
+ * queries with 16-bit scales run on the matrix-core kernel, other dtype pairs
+ * on the exact-fp32 VALU kernel; the plan depends on which.
  */
 int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
-                                   int64_t D, int64_t s_max, int q_dtype, int64_t num_cus);
+                                   int64_t D, int64_t s_max, int q_dtype, int scale_dtype,
+                                   int64_t num_cus);
 
 /*
  * Workspace (device bytes) kvq_decode_attn needs for `n_split` splits. The
@@ -111,7 +114,8 @@ int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t S
  * same stream. Calls that overlap in time must not share a workspace.
  */
 int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
-                                        int64_t D, int q_dtype, int64_t n_split);
+                                        int64_t D, int q_dtype, int scale_dtype,
+                                        int64_t n_split);
 
 /*
  * kvq_decode_attn — fused INT4 GQA attention for short query blocks (decode).

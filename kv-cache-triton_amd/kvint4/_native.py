@@ -61,9 +61,9 @@ def _declare(lib: ctypes.CDLL) -> None:
         _vp, _i32, _i64p, _i64, _vp,
     ]
     lib.kvq_decode_attn_num_splits.restype = _i64
-    lib.kvq_decode_attn_num_splits.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64]
+    lib.kvq_decode_attn_num_splits.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64]
     lib.kvq_decode_attn_workspace_bytes.restype = _i64
-    lib.kvq_decode_attn_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _i64, _i32, _i64]
+    lib.kvq_decode_attn_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64]
     lib.kvq_decode_attn.restype = _i32
     lib.kvq_decode_attn.argtypes = [
         _vp, _i32, _i64p,

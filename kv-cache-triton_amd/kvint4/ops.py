@@ -228,10 +228,12 @@ def fused_decode_attention(
     sm_scale: float,
     seq_lens: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    n_split: int | None = None,
 ) -> torch.Tensor:
     """Launch the fused split-K decode kernel; raises KVQUnsupported for shapes
     it does not handle. q [B, Hq, Sq, D]; K/V codes [B, Hkv, Sk, W] (strided views
-    of a larger cache are fine as long as the last dim is contiguous)."""
+    of a larger cache are fine as long as the last dim is contiguous).
+    `n_split` overrides the planner's sequence-split count (tuning)."""
     B, Hq, Sq, D = q.shape
     Sk = k_packed.shape[2]
     if out is None:
@@ -252,10 +254,14 @@ def fused_decode_attention(
         sl_ptr = seq_lens.data_ptr()
     lib = nat.lib()
     qd = nat.DTYPE_CODE[q.dtype]
-    n_split = lib.kvq_decode_attn_num_splits(B, Hq, n_kv_heads, Sq, D, Sk, qd, _num_cus(q.device))
-    if n_split < 0:
-        nat.check(int(n_split), "kvq_decode_attn_num_splits")
-    ws_bytes = lib.kvq_decode_attn_workspace_bytes(B, Hq, n_kv_heads, Sq, D, qd, n_split)
+    sd = nat.DTYPE_CODE[k_scales.dtype]
+    if n_split is None:
+        n_split = lib.kvq_decode_attn_num_splits(B, Hq, n_kv_heads, Sq, D, Sk, qd, sd, _num_cus(q.device))
+        if n_split < 0:
+            nat.check(int(n_split), "kvq_decode_attn_num_splits")
+    elif n_split < 1:
+        raise ValueError("n_split must be >= 1")
+    ws_bytes = lib.kvq_decode_attn_workspace_bytes(B, Hq, n_kv_heads, Sq, D, qd, sd, n_split)
     if ws_bytes < 0:
         nat.check(int(ws_bytes), "kvq_decode_attn_workspace_bytes")
     with nat.device_of(q):
@@ -270,7 +276,7 @@ def fused_decode_attention(
             k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:3]),
             v_packed.data_ptr(), nat.i64_array(v_packed.stride()[:3]),
             v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:3]),
-            nat.DTYPE_CODE[k_scales.dtype],
+            sd,
             out.data_ptr(), nat.i64_array(out.stride()),
             B, Hq, n_kv_heads, Sq, D, group_size, Sk,
             sl_ptr, 1 if is_causal else 0, float(sm_scale),

@@ -7,10 +7,13 @@ protocol, ragged appends.
 
 Model glue (tests/llama3/test_llama3_quant_decode.py:21-122,
 tests/llama3/test_llama3_generate_parity.py:52-74): a tiny random-init Llama
-(and GPT-2) swapped to the INT4 path on the GPU vs the stock model with a
-DynamicCache on the CPU (bf16 batched products stay off the GPU), with the
-reference's own bars: prefill last-logit max-abs < 1.0 and same argmax, 8
-decode steps < 2.0, greedy prefix agreement >= 4 of 16.
+(and GPT-2) swapped to the INT4 path vs the same stock model with a
+DynamicCache, both on the GPU. The stock model attends through an fp32
+reference attention (tests/_hf_ref.py) so that no half-precision batched GEMM
+runs on the GPU; everything else is the same kernels, so the comparison
+isolates the INT4 KV. Bars are the reference's own: prefill last-logit
+max-abs < 1.0 and same argmax, 8 decode steps < 2.0, greedy prefix agreement
+>= 4 of 16.
 """
 
 from __future__ import annotations
@@ -26,6 +29,8 @@ from kvint4.gpt2.kv_cache import QuantizedKVCache as GPT2Cache
 from kvint4.llama3.kv_cache import QuantizedKVCache
 from kvint4.llama3.llama3_quant import LlamaAttentionQuantized, replace_llama_attention_with_quantized
 from oracle import kvq_oracle as O
+
+from _hf_ref import use_fp32_reference_attention
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -93,27 +98,36 @@ def _tiny_llama(dtype=torch.bfloat16):
     return LlamaForCausalLM(cfg).to(dtype=dtype).eval()
 
 
-def test_llama_prefill_decode_matches_reference():
-    ref = _tiny_llama()                      # stock model, DynamicCache, CPU
+def _pair():
+    """(stock reference, INT4-swapped) tiny Llamas with identical weights, on the GPU."""
+    ref = _tiny_llama()
     quant = _tiny_llama()
     quant.load_state_dict(ref.state_dict())
+    use_fp32_reference_attention(ref)
     replace_llama_attention_with_quantized(quant, group_size=32)
-    quant = quant.to(DEV)
+    return ref.to(DEV), quant.to(DEV)
+
+
+def test_llama_prefill_decode_matches_reference():
+    ref, quant = _pair()
     assert all(isinstance(l.self_attn, LlamaAttentionQuantized) for l in quant.model.layers)
     torch.manual_seed(123)
-    prompt = torch.randint(0, 256, (1, 32))
+    prompt = torch.randint(0, 256, (1, 32), device=DEV)
     with torch.no_grad():
         cache_ref, cache_q = DynamicCache(), QuantizedKVCache(group_size=32)
         out_r = ref(input_ids=prompt, past_key_values=cache_ref, use_cache=True)
-        out_q = quant(input_ids=prompt.to(DEV), past_key_values=cache_q, use_cache=True)
-        lr, lq = out_r.logits[:, -1].float(), out_q.logits[:, -1].float().cpu()
-        assert (lr - lq).abs().max().item() < 1.0
+        out_q = quant(input_ids=prompt, past_key_values=cache_q, use_cache=True)
+        lr, lq = out_r.logits[:, -1].float(), out_q.logits[:, -1].float()
+        d0 = (lr - lq).abs().max().item()
+        print(f"prefill last-logit max-abs diff {d0:.4f}")
+        assert d0 < 1.0
         assert lr.argmax(-1).item() == lq.argmax(-1).item()
         for step in range(8):
-            nid = torch.randint(0, 256, (1, 1))
+            nid = torch.randint(0, 256, (1, 1), device=DEV)
             out_r = ref(input_ids=nid, past_key_values=cache_ref, use_cache=True)
-            out_q = quant(input_ids=nid.to(DEV), past_key_values=cache_q, use_cache=True)
-            d = (out_r.logits[:, -1].float() - out_q.logits[:, -1].float().cpu()).abs().max().item()
+            out_q = quant(input_ids=nid, past_key_values=cache_q, use_cache=True)
+            d = (out_r.logits[:, -1].float() - out_q.logits[:, -1].float()).abs().max().item()
+            print(f"decode step {step} last-logit max-abs diff {d:.4f}")
             assert d < 2.0, f"decode step {step}: {d}"
     assert cache_q.get_seq_length(0) == 40
     seq = 40
@@ -121,18 +135,16 @@ def test_llama_prefill_decode_matches_reference():
 
 
 def test_llama_greedy_prefix_agreement():
-    ref = _tiny_llama()
-    quant = _tiny_llama()
-    quant.load_state_dict(ref.state_dict())
-    replace_llama_attention_with_quantized(quant)
-    quant = quant.to(DEV)
+    ref, quant = _pair()
     torch.manual_seed(321)
-    prompt = torch.randint(0, 256, (1, 24))
+    prompt = torch.randint(0, 256, (1, 24), device=DEV)
 
     def greedy(model, dev, cache, n):
         toks = []
         with torch.no_grad():
-            out = model(input_ids=prompt.to(dev), past_key_values=cache, use_cache=True)
+            out = model(input_ids=prompt, past_key_values=cache, use_cache=True)
+            top2 = out.logits[0, -1].float().topk(2).values
+            print(f"first-token top-2 logit gap {float(top2[0] - top2[1]):.4f}")
             nid = out.logits[:, -1].argmax(-1, keepdim=True)
             toks.append(int(nid.item()))
             for _ in range(n - 1):
@@ -141,7 +153,7 @@ def test_llama_greedy_prefix_agreement():
                 toks.append(int(nid.item()))
         return toks
 
-    a = greedy(ref, "cpu", DynamicCache(), 16)
+    a = greedy(ref, DEV, DynamicCache(), 16)
     b = greedy(quant, DEV, QuantizedKVCache(), 16)
     agree = next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), 16)
     assert agree >= 4, (a, b)
@@ -150,21 +162,22 @@ def test_llama_greedy_prefix_agreement():
 def test_gpt2_random_init_decode_matches_reference():
     cfg = GPT2Config(n_layer=2, n_head=4, n_embd=128, vocab_size=256, n_positions=256)
     torch.manual_seed(0)
-    ref = GPT2LMHeadModel(cfg).eval()                       # fp32, CPU, DynamicCache
+    ref = GPT2LMHeadModel(cfg).eval()                       # fp32, DynamicCache
     quant = GPT2LMHeadModel(cfg).eval()
     quant.load_state_dict(ref.state_dict())
+    use_fp32_reference_attention(ref)
     replace_gpt2_attention_with_quantized(quant)
-    quant = quant.to(DEV)
+    ref, quant = ref.to(DEV), quant.to(DEV)
     torch.manual_seed(7)
-    prompt = torch.randint(0, 256, (1, 20))
+    prompt = torch.randint(0, 256, (1, 20), device=DEV)
     with torch.no_grad():
         cr, cq = DynamicCache(), GPT2Cache()
         lr = ref(input_ids=prompt, past_key_values=cr, use_cache=True).logits[:, -1]
-        lq = quant(input_ids=prompt.to(DEV), past_key_values=cq, use_cache=True).logits[:, -1].cpu()
+        lq = quant(input_ids=prompt, past_key_values=cq, use_cache=True).logits[:, -1]
         assert (lr - lq).abs().max().item() < 1.0 and lr.argmax().item() == lq.argmax().item()
         for _ in range(6):
-            nid = torch.randint(0, 256, (1, 1))
+            nid = torch.randint(0, 256, (1, 1), device=DEV)
             lr = ref(input_ids=nid, past_key_values=cr, use_cache=True).logits[:, -1]
-            lq = quant(input_ids=nid.to(DEV), past_key_values=cq, use_cache=True).logits[:, -1].cpu()
+            lq = quant(input_ids=nid, past_key_values=cq, use_cache=True).logits[:, -1]
             assert (lr - lq).abs().max().item() < 2.0
     assert cq.get_seq_length(0) == 26
