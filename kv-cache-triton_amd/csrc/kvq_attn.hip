@@ -9,10 +9,13 @@
 // workgroup owns one (batch, kv head, query-row chunk) and one slice of the
 // sequence (split-K): every query head of the GQA group (times the Sq query
 // positions) is a "row" processed against the same K/V bytes, so each cache
-// byte crosses HBM once, and B*Hkv*n_split workgroups fill the CUs. Partial
-// (max, sum, o) triples are merged across the 4 waves of a workgroup in LDS and
-// then across splits by the last workgroup of the unit (device-scope counter),
-// which writes the output.
+// byte crosses HBM once, and B*Hkv*n_split workgroups fill the CUs. Splits are
+// balanced to the token (split s of a sequence of L keys covers
+// [s*L/n_split, (s+1)*L/n_split)), so ragged batches stay balanced too. Partial
+// (max, sum, o) triples are merged across the waves of a workgroup in LDS and
+// then across splits by the last workgroup of the unit to finish (device-scope
+// release fence + atomic counter, acquire fence), which writes the output and
+// re-arms the counter.
 //
 // Two kernels share that frame:
 //
@@ -60,10 +63,11 @@ struct AttnArgs {
   int64_t os_b, os_h, os_s, os_d;
   const int32_t* seq_lens;
   int Hkv, Sq, G, Sk, ratio, rows_total, row_chunks, n_units;
-  int n_split, split_len, causal, scale_dtype, xcd_remap, q_vec;
+  int n_split, causal, scale_dtype, xcd_remap, q_vec;
   float scale_log2;
-  float* ws_ml;  // [n_units][n_split][ROWS][2]  (max, sum)
-  float* ws_o;   // [n_units][n_split][ROWS][D]
+  uint32_t* ws_cnt;  // [n_units] arrival counters (zero between calls)
+  float* ws_ml;      // [n_units][n_split][ROWS][2]  (max, sum)
+  float* ws_o;       // [n_units][n_split][ROWS][D]
 };
 
 constexpr float kNeg = -1.0e30f;
@@ -163,16 +167,91 @@ __device__ __forceinline__ int64_t out_index(const AttnArgs& a, int b, int kvh, 
   return (int64_t)b * a.os_b + (int64_t)head * a.os_h + (int64_t)qi * a.os_s + (int64_t)d * a.os_d;
 }
 
+// Token range [t0, t1) of split `split` over a sequence of L keys.
+__device__ __forceinline__ void split_range(const AttnArgs& a, int L, int split, int& t0, int& t1) {
+  t0 = (int)(((int64_t)split * L) / a.n_split);
+  t1 = (int)(((int64_t)(split + 1) * L) / a.n_split);
+}
+
+constexpr int kMaxRows = 8;  // query rows per workgroup (both kernels)
+
 struct MergeLds {
-  float l[8];
-  float m[8];
-  float wf[8][8];  // per-wave rescale factors 2^(m_wave - M)
+  float l[kMaxRows];
+  float m[kMaxRows];
+  float wf[8][kMaxRows];           // per-wave rescale factors 2^(m_wave - M)
+  int last;                        // this workgroup merges the unit's splits
 };
+
+// Partials cross between workgroups that may sit on different XCDs (each with
+// its own L2), so they are written and read with device-scope accesses (the
+// sc1 cache policy: stores write through to the device-coherent level, loads
+// do not hit a stale L2 copy). That needs no L2 writeback or invalidate, which
+// a device-scope fence would issue.
+__device__ __forceinline__ void ws_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ws_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cross-split merge, run by the last workgroup of a unit to finish: out =
+// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. Each
+// thread owns (row, dim) outputs and issues the loads of all partials it needs
+// (the row's (max, sum) pairs and its o values, BATCH splits at a time) before
+// using any of them, so the merge costs one round trip per BATCH splits. A row
+// no split saw a key for (all l_s = 0) yields zeros.
+template <int ROWS, int D, int OUT_DT, int NW>
+__device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc, int kvh, int b) {
+  constexpr int NT = 64 * NW;
+  constexpr int BATCH = 32;
+  const int ns = a.n_split;
+  const int64_t slot0 = (int64_t)unit * ns * ROWS;  // + split * ROWS + row
+  for (int idx = threadIdx.x; idx < ROWS * D; idx += NT) {
+    const int r = idx / D, d = idx % D;
+    const float* mlb = a.ws_ml + 2 * (slot0 + r);
+    const float* ob = a.ws_o + (slot0 + r) * D + d;
+    const int64_t ml_step = 2 * ROWS, o_step = (int64_t)ROWS * D;
+    float M = kNeg, Ls = 0.0f, acc = 0.0f;
+    for (int sp0 = 0; sp0 < ns; sp0 += BATCH) {
+      float mv[BATCH], lv[BATCH], ov[BATCH];
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        const int64_t sp = min(sp0 + j, ns - 1);
+        mv[j] = ws_load(mlb + sp * ml_step);
+        lv[j] = ws_load(mlb + sp * ml_step + 1);
+        ov[j] = ws_load(ob + sp * o_step);
+      }
+      float Mb = M;
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j)
+        if (sp0 + j < ns) Mb = fmaxf(Mb, mv[j]);
+      const float f = __builtin_amdgcn_exp2f(M - Mb);
+      Ls *= f;
+      acc *= f;
+      M = Mb;
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        if (sp0 + j < ns) {
+          const float w = __builtin_amdgcn_exp2f(mv[j] - M);
+          Ls = fmaf(lv[j], w, Ls);
+          acc = fmaf(ov[j], w, acc);
+        }
+      }
+    }
+    const int rho = rc * ROWS + r;
+    if (rho < a.rows_total)
+      store_from_f32(a.out, out_index(a, b, kvh, rho, d), OUT_DT, Ls > 0.0f ? acc / Ls : 0.0f);
+  }
+}
 
 // Merge the partials of the NW waves — NW * PPW partial slots in o_lds, slot p
 // belonging to wave p / PPW, with (max, sum) per wave in ml_lds; the caller
 // has already passed a barrier — and store either the output (single split) or
-// this split's partial (max, sum, o) for decode_attn_merge_kernel.
+// this split's partial (max, sum, o). With several splits the partial is then
+// published: every wave waits until its device-scope partial stores are
+// complete, and after a barrier one thread bumps the unit's arrival counter
+// (a system-scope atomic, performed at the memory side). The workgroup that
+// arrives last merges all partials and re-arms the counter for the next call.
 template <int ROWS, int D, int OUT_DT, int NW, int PPW>
 __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int split, int rc,
                                              int kvh, int b, const float (*o_lds)[ROWS][D],
@@ -207,66 +286,25 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
         store_from_f32(a.out, out_index(a, b, kvh, rho, d), OUT_DT, Ls > 0.0f ? Os / Ls : 0.0f);
     } else {
       const int64_t slot = ((int64_t)unit * a.n_split + split) * ROWS + r;
-      a.ws_o[slot * D + d] = Os;
+      ws_store(a.ws_o + slot * D + d, Os);
       if (d == 0) {
-        a.ws_ml[slot * 2 + 0] = mg.m[r];
-        a.ws_ml[slot * 2 + 1] = Ls;
+        ws_store(a.ws_ml + slot * 2 + 0, mg.m[r]);
+        ws_store(a.ws_ml + slot * 2 + 1, Ls);
       }
     }
   }
-}
-
-// Split-K merge, launched after the attention kernel on the same stream (the
-// kernel boundary orders the partials' stores before these loads). One thread
-// per (unit, row, dim): out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s,
-// M = max_s m_s, over the n_split partials, BATCH of them per round of loads.
-// A row no split saw a key for (all l_s = 0) yields zeros.
-template <int OUT_DT>
-__global__ __launch_bounds__(128) void decode_attn_merge_kernel(const AttnArgs a, int rows, int D) {
-  constexpr int BATCH = 32;
-  const int64_t gid = (int64_t)blockIdx.x * 128 + threadIdx.x;
-  if (gid >= (int64_t)a.n_units * rows * D) return;
-  const int d = (int)(gid % D);
-  const int64_t ur = gid / D;
-  const int r = (int)(ur % rows);
-  const int unit = (int)(ur / rows);
-  const int rc = unit % a.row_chunks;
-  const int bh = unit / a.row_chunks;
-  const int kvh = bh % a.Hkv, b = bh / a.Hkv;
-  const int rho = rc * rows + r;
-  if (rho >= a.rows_total) return;
-  const int64_t slot0 = (int64_t)unit * a.n_split * rows + r;  // + split * rows
-  const float2* ml2 = (const float2*)a.ws_ml + slot0;
-  const float* ob = a.ws_o + slot0 * D + d;
-  const int64_t o_step = (int64_t)rows * D;
-  float M = kNeg, Ls = 0.0f, acc = 0.0f;
-  for (int sp0 = 0; sp0 < a.n_split; sp0 += BATCH) {
-    float2 ml[BATCH];
-    float ov[BATCH];
-#pragma unroll
-    for (int j = 0; j < BATCH; ++j) {
-      const int64_t sp = min(sp0 + j, a.n_split - 1);
-      ml[j] = ml2[sp * rows];
-      ov[j] = ob[sp * o_step];
-    }
-    float Mb = M;
-#pragma unroll
-    for (int j = 0; j < BATCH; ++j)
-      if (sp0 + j < a.n_split) Mb = fmaxf(Mb, ml[j].x);
-    const float f = __builtin_amdgcn_exp2f(M - Mb);
-    Ls *= f;
-    acc *= f;
-    M = Mb;
-#pragma unroll
-    for (int j = 0; j < BATCH; ++j) {
-      if (sp0 + j < a.n_split) {
-        const float w = __builtin_amdgcn_exp2f(ml[j].x - M);
-        Ls = fmaf(ml[j].y, w, Ls);
-        acc = fmaf(ov[j], w, acc);
-      }
-    }
+  if (single) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are complete
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(a.ws_cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    mg.last = prev == (uint32_t)(a.n_split - 1) ? 1 : 0;
   }
-  store_from_f32(a.out, out_index(a, b, kvh, rho, d), OUT_DT, Ls > 0.0f ? acc / Ls : 0.0f);
+  __syncthreads();
+  if (!mg.last) return;
+  merge_splits<ROWS, D, OUT_DT, NW>(a, unit, rc, kvh, b);
+  if (tid == 0) __hip_atomic_store(a.ws_cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // ===========================================================================
@@ -289,15 +327,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int D, int RS, int QM, bool ROWMASK, int NW>
+template <int D, int RS, int QM, bool ROWMASK, int NW, int CH>
 __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArgs a) {
   constexpr bool F16 = QM == KVQ_F16;
-  constexpr int LPT = D / 32;     // 32-dim chunks per token
-  constexpr int VLPT = D / 8;     // V lanes per token row (one dword each)
-  constexpr int VTS = 64 / VLPT;  // V token subsets
-  constexpr int SUB = 4 * VTS;    // tokens per V sub-tile
-  constexpr int NSUB = 64 / SUB;  // V sub-tiles per 64-token tile
-  constexpr int CH = NW == 8 ? 1 : 2;  // tiles per wave per chunk (all their loads in flight)
+  constexpr int LPT = D / 32;       // 32-dim chunks (16 code bytes) per token
+  constexpr int VROW = D / 2;       // code bytes per token row
+  constexpr int VLD = VROW * 64 / 1024;  // 16-byte V loads per lane per 64-token tile
+  constexpr int VLPT = D / 8;       // PV lanes per token row (one code dword each)
+  constexpr int VTS = 64 / VLPT;    // PV token subsets
+  constexpr int SUB = 4 * VTS;      // tokens per PV sub-tile
+  constexpr int NSUB = 64 / SUB;    // PV sub-tiles per 64-token tile
   constexpr int ROWS = 4 * RS;
   constexpr int QT = ROWS * D / 8;  // threads staging the query rows, 8 elements each
   constexpr uint32_t MAGIC = F16 ? 0x64646464u : 0x43434343u;
@@ -306,17 +345,25 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   constexpr uint32_t SEL_46 = 0x04030402u;  // {MAGIC | byte2, MAGIC | byte3}
   static_assert(QT <= 64 * NW, "query staging");
 
+  // Per wave: the V codes of the tile being consumed (row-major image of the
+  // tile, 64 x VROW bytes) and its softmax weights [rowset][row][chunk]
+  // [subtile][tsub][4 tokens]. Once the sequence loop is done the same bytes
+  // hold the per-wave partial outputs.
+  constexpr int V_BYTES = NW * 64 * VROW;
+  constexpr int W_BYTES = NW * RS * 4 * LPT * NSUB * VTS * 4 * 2;
+  constexpr int O_BYTES = NW * ROWS * D * 4;
+  constexpr int S_BYTES = V_BYTES + W_BYTES > O_BYTES ? V_BYTES + W_BYTES : O_BYTES;
   __shared__ __attribute__((aligned(16))) uint32_t q_lds[ROWS][D / 2];
-  // softmax weights, per wave: [tile][rowset][row][chunk][subtile][tsub][4 tokens]
-  __shared__ __attribute__((aligned(16))) uint16_t w_lds[NW][CH][RS][4][LPT][NSUB][VTS][4];
-  // partial outputs, one slot per (wave, token subset)
-  __shared__ __attribute__((aligned(16))) float o_lds[NW * VTS][ROWS][D];
+  __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
   __shared__ float ml_lds[NW][ROWS][2];
   __shared__ MergeLds mg;
+  auto v_lds = reinterpret_cast<uint8_t(*)[64 * VROW]>(smem);
+  auto w_lds = reinterpret_cast<uint16_t(*)[RS][4][LPT][NSUB][VTS][4]>(smem + V_BYTES);
+  auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   int unit, split;
   unit_and_split(a, unit, split);
   const int rc = unit % a.row_chunks;
@@ -329,28 +376,9 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     const int sl = a.seq_lens[b];
     L = sl < 0 ? 0 : (sl < a.Sk ? sl : a.Sk);
   }
-  const int t_begin = split * a.split_len;
-  const int t_end = min(t_begin + a.split_len, L);
+  int t_begin, t_end;
+  split_range(a, L, split, t_begin, t_end);
   const int ntiles = t_end > t_begin ? (t_end - t_begin + 63) / 64 : 0;
-
-  // ---- query staging loads go out first: thread (q_r, q_k) of every wave
-  //      reads elements [8 q_k, 8 q_k + 8) of row q_r with 16-bit loads (no
-  //      branch, so the compiler can wait for them alone later); rows past
-  //      the last one read row 0 and are zeroed ----
-  const int q_r = (tid % QT) / (D / 8), q_k = tid % (D / 8);
-  const int q_rho = rc * ROWS + q_r;
-  const bool q_ok = q_rho < a.rows_total;
-  uint32_t qe[8];
-  {
-    const int rho = q_ok ? q_rho : 0;
-    const int head = kvh * a.ratio + rho / a.Sq, qi = rho % a.Sq;
-    const uint16_t* q16 = (const uint16_t*)a.q +
-                          ((int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
-                           (int64_t)(8 * q_k) * a.qs_d);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qe[j] = q16[(int64_t)j * a.qs_d];
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep the query loads ahead of the cache loads
 
   // ---- cache slices as bounds-checked buffers (rows >= L read as zero) ----
   const uint8_t* kp_bh = a.kp + (int64_t)b * a.kps_b + (int64_t)kvh * a.kps_h;
@@ -359,17 +387,19 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const uint16_t* vs_bh = (const uint16_t*)a.vs + ((int64_t)b * a.vss_b + (int64_t)kvh * a.vss_h);
   const uint32_t kps = (uint32_t)a.kps_s, vps = (uint32_t)a.vps_s;
   const uint32_t kss2 = 2u * (uint32_t)a.kss_s, vss2 = 2u * (uint32_t)a.vss_s;
-  const uint32_t Lu = (uint32_t)L;
-  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kp_bh, Lu * kps);
-  const __amdgpu_buffer_rsrc_t rks = buffer_rsrc(ks_bh, Lu * kss2);
-  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vp_bh, Lu * vps);
-  const __amdgpu_buffer_rsrc_t rvs = buffer_rsrc(vs_bh, Lu * vss2);
+  // Rows at or past this split's end read as zero and move no bytes.
+  const uint32_t Le = (uint32_t)t_end;
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kp_bh, Le * kps);
+  const __amdgpu_buffer_rsrc_t rks = buffer_rsrc(ks_bh, Le * kss2);
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vp_bh, Le * vps);
+  const __amdgpu_buffer_rsrc_t rvs = buffer_rsrc(vs_bh, Le * vss2);
   const bool s_f16 = a.scale_dtype == KVQ_F16;
-  uint32_t goff[LPT];  // byte offset of each 32-dim chunk's scale in a row
+  const int ng = (D + a.G - 1) / a.G;  // scales per token row: 1, 2 or 4 (wave-uniform)
+  uint32_t gsh[LPT];  // bit offset of each 32-dim chunk's scale in the loaded scale row
 #pragma unroll
-  for (int c = 0; c < LPT; ++c) goff[c] = 2u * (uint32_t)((c * 32) / a.G);
+  for (int c = 0; c < LPT; ++c) gsh[c] = 16u * (uint32_t)((c * 32) / a.G);
 
-  // V lane layout and the LDS slot this lane's token fills
+  // PV lane layout and the LDS slot this lane's token fills
   const int vts = lane / VLPT;
   const int vj = lane % VLPT;
   const int v_row = vj & 3;   // A-operand row of this lane's block
@@ -377,56 +407,83 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const int w_sub = lane / SUB;             // sub-tile of token `lane`
   const int w_ts = (lane % SUB) % VTS;      // its token subset
   const int w_k = (lane % SUB) / VTS;       // its position in the subset
+  // V loads: load j of a lane covers bytes [1024 j + 16 lane, +16) of the
+  // tile's row-major image: token (1024 j + 16 lane) / VROW of the tile.
+  uint32_t v_tok[VLD], v_off[VLD];
+#pragma unroll
+  for (int j = 0; j < VLD; ++j) {
+    v_tok[j] = (uint32_t)((1024 * j + 16 * lane) / VROW);
+    v_off[j] = (uint32_t)((1024 * j + 16 * lane) % VROW);
+  }
 
-  // Chunk registers (CH tiles of 64 tokens). Tile i of a chunk is computed
+  // Register slots for CH tiles of 64 tokens. Tile i of a chunk is computed
   // start to finish before tile i + 1, and each of its parts is refilled for
   // the next chunk as soon as it is consumed, so loads overlap the math.
+  // Per tile and lane: the lane's token's K row (LPT x 16 bytes), its K and V
+  // scale rows (one 2/4/8-byte load each) and VLD 16-byte pieces of the V
+  // tile — 6 to 10 wide loads per tile and wave.
   u32x4_t kc4[CH][LPT];
-  uint32_t skr[CH][LPT], svr[CH][LPT];
-  uint32_t vcode[CH][NSUB][4];
-  // Loads are never behind a branch (the compiler's wait counting stays exact
-  // across them); a load that is not needed gets an offset past every buffer
-  // (kOob) and returns zero without touching memory.
-  constexpr uint32_t kOob = 0x80000000u;
-  auto load_k = [&](int i, int base, bool live) {
-    const uint32_t t = (uint32_t)(t_begin + (base + NW * i) * 64 + lane);
-    const uint32_t ko = live ? t * kps : kOob, so = live ? t * kss2 : kOob;
-#pragma unroll
-    for (int c = 0; c < LPT; ++c) {
-      kc4[i][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16u * c, 0, 0));
-      skr[i][c] = __builtin_amdgcn_raw_buffer_load_b16(rks, so + goff[c], 0, 0);
-    }
+  uint2 skr[CH], svr[CH];
+  u32x4_t vq[CH][VLD];
+  auto load_scales = [&](__amdgpu_buffer_rsrc_t r, uint32_t off) -> uint2 {
+    if (ng >= 4) return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    if (ng == 2) return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0), 0u);
+    return make_uint2(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0), 0u);
   };
-  auto load_vs = [&](int i, int base, bool live) {
-    const uint32_t so = live ? (uint32_t)(t_begin + (base + NW * i) * 64 + lane) * vss2 : kOob;
+  auto tile_t0 = [&](int i, int base) { return (uint32_t)(t_begin + (base + NW * i) * 64); };
+  auto load_k = [&](int i, int base) {
+    const uint32_t t = tile_t0(i, base) + lane;
 #pragma unroll
-    for (int c = 0; c < LPT; ++c) svr[i][c] = __builtin_amdgcn_raw_buffer_load_b16(rvs, so + goff[c], 0, 0);
+    for (int c = 0; c < LPT; ++c)
+      kc4[i][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, t * kps + 16u * c, 0, 0));
+    skr[i] = load_scales(rks, t * kss2);
   };
-  auto load_v = [&](int i, int base, bool live) {
-    const uint32_t vo = live ? (uint32_t)(t_begin + (base + NW * i) * 64 + vts) * vps + 4u * vj : kOob;
+  auto load_v = [&](int i, int base) {
+    const uint32_t t0 = tile_t0(i, base);
+    svr[i] = load_scales(rvs, (t0 + lane) * vss2);
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        vcode[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + (uint32_t)(s * SUB + VTS * k) * vps, 0, 0);
-    }
-  };
-  auto load_tile = [&](int i, int base, bool live) {
-    load_k(i, base, live);
-    load_vs(i, base, live);
-    load_v(i, base, live);
+    for (int j = 0; j < VLD; ++j)
+      vq[i][j] = __builtin_bit_cast(u32x4_t,
+                                    __builtin_amdgcn_raw_buffer_load_b128(rv, (t0 + v_tok[j]) * vps + v_off[j], 0, 0));
   };
   // With one row set the first chunk's loads go out before the query is
-  // processed; two row sets have no registers to spare for that and load each
-  // chunk at the top of the loop.
+  // staged; two row sets load each chunk at the top of the loop.
   constexpr bool PIPE = RS == 1;
   if constexpr (PIPE) {
 #pragma unroll
-    for (int i = 0; i < CH; ++i) load_tile(i, wave, wave + NW * i < ntiles);
+    for (int i = 0; i < CH; ++i) {
+      if (wave + NW * i < ntiles) {
+        load_k(i, wave);
+        load_v(i, wave);
+      }
+    }
   }
 
-  // ---- query rows -> LDS, permuted to the key operand order ----
+  // ---- query rows -> LDS, permuted to the key operand order: thread (q_r,
+  //      q_k) < QT stages elements [8 q_k, 8 q_k + 8) of row q_r; rows past
+  //      the last one are zeros ----
   if (tid < QT) {
+    const int q_r = tid / (D / 8), q_k = tid % (D / 8);
+    const int q_rho = rc * ROWS + q_r;
+    const bool q_ok = q_rho < a.rows_total;
+    const int rho = q_ok ? q_rho : 0;
+    const int head = kvh * a.ratio + rho / a.Sq, qi = rho % a.Sq;
+    const int64_t qoff = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
+                         (int64_t)(8 * q_k) * a.qs_d;
+    uint32_t qe[8];
+    if (a.q_vec) {
+      const uint4 w = *(const uint4*)((const uint16_t*)a.q + qoff);
+      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qe[2 * j] = wd[j] & 0xffffu;
+        qe[2 * j + 1] = wd[j] >> 16;
+      }
+    } else {
+      const uint16_t* q16 = (const uint16_t*)a.q + qoff;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qe[j] = q16[(int64_t)j * a.qs_d];
+    }
     const uint32_t keep = q_ok ? 0xffffu : 0u;
     const u32x4_t qp = {(qe[0] & keep) | ((qe[2] & keep) << 16), (qe[1] & keep) | ((qe[3] & keep) << 16),
                         (qe[4] & keep) | ((qe[6] & keep) << 16), (qe[5] & keep) | ((qe[7] & keep) << 16)};
@@ -476,14 +533,21 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     w_acc[rs] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
+  uint8_t* my_v = v_lds[wave];
   for (int base = wave; base < ntiles; base += NW * CH) {
     if constexpr (!PIPE) {
 #pragma unroll
-      for (int i = 0; i < CH; ++i) load_tile(i, base, base + NW * i < ntiles);
+      for (int i = 0; i < CH; ++i) {
+        if (base + NW * i < ntiles) {
+          load_k(i, base);
+          load_v(i, base);
+        }
+      }
     }
-    const bool more = PIPE && base + NW * CH < ntiles;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
+      if (base + NW * i >= ntiles) break;  // wave-uniform: this wave has no tile i
+      const bool refill = PIPE && base + NW * (CH + i) < ntiles;
       // ---- QK on the matrix cores: scores of token `lane` for every row ----
       float sc[RS][4];
       {
@@ -512,10 +576,12 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
           }
         }
         const int t = t_begin + (base + NW * i) * 64 + lane;
-        const bool tok_ok = (base + NW * i < ntiles) && (t < t_end);
+        const bool tok_ok = t < t_end;
+        const uint64_t skw = ((uint64_t)skr[i].y << 32) | skr[i].x;
         float skl[LPT];
 #pragma unroll
-        for (int c = 0; c < LPT; ++c) skl[c] = scale16_to_f32(skr[i][c], s_f16) * a.scale_log2;
+        for (int c = 0; c < LPT; ++c)
+          skl[c] = scale16_to_f32((uint32_t)(skw >> gsh[c]) & 0xffffu, s_f16) * a.scale_log2;
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
@@ -529,7 +595,11 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
           }
         }
       }
-      load_k(i, base + NW * CH, more && base + NW * (CH + i) < ntiles);
+      if (refill) load_k(i, base + NW * CH);
+
+      // ---- V codes of this tile -> the wave's LDS image ----
+#pragma unroll
+      for (int j = 0; j < VLD; ++j) *(u32x4_t*)&my_v[1024 * j + 16 * lane] = vq[i][j];
 
       // ---- tile max and rescale of the running state ----
       bool grow = false;
@@ -560,9 +630,10 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
 
       // ---- p and w = p * v_scale (bf16) -> LDS ----
       {
+        const uint64_t svw = ((uint64_t)svr[i].y << 32) | svr[i].x;
         float svl[LPT];
 #pragma unroll
-        for (int c = 0; c < LPT; ++c) svl[c] = scale16_to_f32(svr[i][c], s_f16);
+        for (int c = 0; c < LPT; ++c) svl[c] = scale16_to_f32((uint32_t)(svw >> gsh[c]) & 0xffffu, s_f16);
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
@@ -572,11 +643,11 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
             l_acc[rs][r] += p;
 #pragma unroll
             for (int c = 0; c < LPT; ++c)
-              w_lds[wave][i][rs][r][c][w_sub][w_ts][w_k] = __builtin_bit_cast(uint16_t, (__bf16)(p * svl[c]));
+              w_lds[wave][rs][r][c][w_sub][w_ts][w_k] = __builtin_bit_cast(uint16_t, (__bf16)(p * svl[c]));
           }
         }
       }
-      load_vs(i, base + NW * CH, more && base + NW * (CH + i) < ntiles);
+      if (refill) load_v(i, base + NW * CH);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -586,10 +657,14 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       // and high nibbles then give (token0, token1) pairs of one dim per perm.
 #pragma unroll
       for (int s = 0; s < NSUB; ++s) {
+        uint32_t vc[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          vc[k] = *(const uint32_t*)&my_v[(s * SUB + VTS * k + vts) * VROW + 4 * vj];
         uint32_t bp[2][8];  // [token pair][dim within the lane's 8]
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
-          const uint32_t v0 = vcode[i][s][2 * tp], v1 = vcode[i][s][2 * tp + 1];
+          const uint32_t v0 = vc[2 * tp], v1 = vc[2 * tp + 1];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {  // dims 0-3, dims 4-7
             const uint32_t u = __builtin_amdgcn_perm(v1, v0, hh ? 0x07030602u : 0x05010400u);
@@ -602,42 +677,65 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
         }
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
-          const uint2 wa = *(const uint2*)&w_lds[wave][i][rs][v_row][v_chunk][s][vts][0];
+          const uint2 wa = *(const uint2*)&w_lds[wave][rs][v_row][v_chunk][s][vts][0];
 #pragma unroll
           for (int m = 0; m < 8; ++m)
             o_acc[rs][m] = mfma4<false>(wa.x, wa.y, bp[0][m], bp[1][m], o_acc[rs][m]);
           w_acc[rs] = mfma4<false>(wa.x, wa.y, kBf16OnePair, kBf16OnePair, w_acc[rs]);
         }
       }
-      load_v(i, base + NW * CH, more && base + NW * (CH + i) < ntiles);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 
-  // ---- wave partial -> LDS: one slot per token subset, o[row][8*vj + m] ----
+  // ---- wave partial: sum over the VTS token subsets (lanes VLPT apart),
+  //      then o[row][8*vj + m] -> LDS (over the V/weight bytes, so every wave
+  //      must be done with those first) ----
+  float ov[RS][4][8];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float* dst = &o_lds[wave * VTS + vts][rs * 4 + r][8 * vj];
-      float v[8];
 #pragma unroll
-      for (int m = 0; m < 8; ++m) v[m] = fmaf(-136.0f, w_acc[rs][r], o_acc[rs][m][r]);
-      *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
-      *(float4*)(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      for (int m = 0; m < 8; ++m) {
+        float v = fmaf(-136.0f, w_acc[rs][r], o_acc[rs][m][r]);
+#pragma unroll
+        for (int step = VLPT; step < 64; step *= 2) v += __shfl_xor(v, step, 64);
+        ov[rs][r][m] = v;
+      }
     }
+  }
+  float lsum[RS][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float lsum = wave_sum(l_acc[rs][r]);
-      if (lane == 0) {
+  for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lsum[rs][r] = wave_sum(l_acc[rs][r]);
+  __syncthreads();
+  if (vts == 0) {
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float* dst = &o_lds[wave][rs * 4 + r][8 * vj];
+        *(float4*)dst = make_float4(ov[rs][r][0], ov[rs][r][1], ov[rs][r][2], ov[rs][r][3]);
+        *(float4*)(dst + 4) = make_float4(ov[rs][r][4], ov[rs][r][5], ov[rs][r][6], ov[rs][r][7]);
+      }
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
         ml_lds[wave][rs * 4 + r][0] = m_run[rs][r];
-        ml_lds[wave][rs * 4 + r][1] = lsum;
+        ml_lds[wave][rs * 4 + r][1] = lsum[rs][r];
       }
     }
   }
   __syncthreads();
-  finish_block<ROWS, D, QM, NW, VTS>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
+  finish_block<ROWS, D, QM, NW, 1>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
 }
 
 // ===========================================================================
@@ -663,7 +761,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   int unit, split;
   unit_and_split(a, unit, split);
   const int rc = unit % a.row_chunks;
@@ -676,8 +774,8 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     const int sl = a.seq_lens[b];
     L = sl < 0 ? 0 : (sl < a.Sk ? sl : a.Sk);
   }
-  const int t_begin = split * a.split_len;
-  const int t_end = min(t_begin + a.split_len, L);
+  int t_begin, t_end;
+  split_range(a, L, split, t_begin, t_end);
   const int ntiles = t_end > t_begin ? (t_end - t_begin + TPT - 1) / TPT : 0;
 
   const int kt = lane / LPT;
@@ -927,7 +1025,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
 
 struct Plan {
   bool mfma;
-  int rows, row_chunks, n_units, n_split, split_len;
+  int rows, row_chunks, n_units, n_split;
 };
 
 // The MFMA kernel serves bf16/fp16 queries with 16-bit scales; everything else
@@ -936,45 +1034,48 @@ static bool use_mfma(int q_dtype, int scale_dtype) {
   return q_dtype != KVQ_F32 && scale_dtype != KVQ_F32;
 }
 
+// Fewest keys a split is given (when the sequence is long enough to split):
+// two 64-token MFMA tiles, or four 16/32-token VALU tiles.
+static int64_t min_split_tokens(bool mfma, int64_t D) { return mfma ? 128 : 4 * (64 / (D / 32)); }
+
+// Split-K plan: enough splits that B * Hkv * row_chunks * n_split workgroups
+// cover the CUs once (one resident workgroup per CU), no split shorter than
+// min_split_tokens of the longest sequence, at most kMaxSplit.
 static int make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, int64_t s_max,
                      int q_dtype, int scale_dtype, int64_t n_split_req, int64_t num_cus, Plan* p) {
   if (B < 1 || Hq < 1 || Hkv < 1 || Sq < 1 || s_max < 0 || Hq % Hkv != 0) return KVQ_EINVAL;
   if (!(D == 64 || D == 128)) return KVQ_EUNSUP;
   const int64_t rows_total = (Hq / Hkv) * Sq;
   p->mfma = use_mfma(q_dtype, scale_dtype);
-  int tpt;  // tokens per wave tile
   if (p->mfma) {
     p->rows = rows_total <= 4 ? 4 : 8;
-    tpt = 64;
   } else {
     const int cap = q_dtype == KVQ_F32 ? 2 : 8;
     int r = 1;
     while (r < rows_total && r < cap) r *= 2;
     p->rows = r;
-    tpt = (int)(64 / (D / 32));
   }
   p->row_chunks = (int)((rows_total + p->rows - 1) / p->rows);
   const int64_t units = B * Hkv * p->row_chunks;
   if (units > (1ll << 30)) return KVQ_EUNSUP;
   p->n_units = (int)units;
-  const int64_t max_split = std::max<int64_t>(1, (s_max + 4 * tpt - 1) / (4 * tpt));
+  const int64_t mst = min_split_tokens(p->mfma, D);
+  const int64_t max_split = std::max<int64_t>(1, s_max / mst);
   int64_t ns = n_split_req;
   if (ns <= 0) {
     const int64_t cus = std::max<int64_t>(1, num_cus);
     ns = (cus + units - 1) / units;
   }
   ns = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ns, max_split), kMaxSplit));
-  int64_t split_len = (s_max + ns - 1) / ns;
-  split_len = std::max<int64_t>(tpt, ((split_len + tpt - 1) / tpt) * tpt);
-  ns = std::max<int64_t>(1, (s_max + split_len - 1) / split_len);
   if (units * ns > 0x7fffffffll || units * p->rows * D / 128 >= 0x7fffffffll) return KVQ_EUNSUP;
   p->n_split = (int)ns;
-  p->split_len = (int)std::min<int64_t>(split_len, 0x7fffffffll);
   return KVQ_OK;
 }
 
-// Workspace: per (unit, split, row) the partial (max, sum) pair, then the
-// partial output row; the (max, sum) block is padded to 256 bytes.
+// Workspace: the per-unit arrival counters (a 256-byte block), per (unit,
+// split, row) the partial (max, sum) pair (padded to 256 bytes), then the
+// partial output rows.
+static int64_t ws_cnt_bytes(const Plan& p) { return ((int64_t)p.n_units * 4 + 255) / 256 * 256; }
 static int64_t ws_ml_bytes(const Plan& p) {
   const int64_t slots = (int64_t)p.n_units * p.n_split * p.rows;
   return (slots * 2 * 4 + 255) / 256 * 256;
@@ -982,20 +1083,22 @@ static int64_t ws_ml_bytes(const Plan& p) {
 
 static int64_t workspace_bytes_for(const Plan& p, int64_t D) {
   if (p.n_split <= 1) return 0;
-  return ws_ml_bytes(p) + (int64_t)p.n_units * p.n_split * p.rows * D * 4;
+  return ws_cnt_bytes(p) + ws_ml_bytes(p) + (int64_t)p.n_units * p.n_split * p.rows * D * 4;
 }
 
-// Waves per workgroup of the MFMA kernel: one row set runs 8 waves of one tile
-// each (two waves per SIMD hide each other's latency); two row sets need more
-// registers than that allows and run 4 waves of two tiles.
+// Waves per workgroup of the MFMA kernel: one row set runs 8 waves (two per
+// SIMD hide each other's latency); two row sets need more registers than that
+// allows and run 4. Each wave keeps the loads of two 64-token tiles in flight.
 template <int RS>
 constexpr int mfma_waves() { return RS == 1 ? 8 : 4; }
+constexpr int kMfmaTilesInFlight = 2;
 
 template <int D, int RS, int QM>
 static void launch_mfma_rs(const AttnArgs& a, bool rowmask, dim3 grid, hipStream_t st) {
   constexpr int NW = mfma_waves<RS>();
-  if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, true, NW>), grid, dim3(64 * NW), 0, st, a);
-  else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, false, NW>), grid, dim3(64 * NW), 0, st, a);
+  constexpr int CH = kMfmaTilesInFlight;
+  if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, true, NW, CH>), grid, dim3(64 * NW), 0, st, a);
+  else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, false, NW, CH>), grid, dim3(64 * NW), 0, st, a);
 }
 
 template <int D, int QM>
@@ -1073,7 +1176,7 @@ extern "C" int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_
   // s_max only bounds n_split in planning; pass one that keeps n_split.
   Plan p;
   const int rc =
-      make_plan(B, Hq, Hkv, Sq, D, n_split * 4 * 64, q_dtype, scale_dtype, n_split, 1, &p);
+      make_plan(B, Hq, Hkv, Sq, D, n_split * 256, q_dtype, scale_dtype, n_split, 1, &p);
   if (rc != KVQ_OK) {
     set_error("kvq_decode_attn_workspace_bytes: unsupported or invalid shape");
     return rc;
@@ -1112,14 +1215,31 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   KVQ_CHECK_ARG(q && out, "kvq_decode_attn: null q/out");
   KVQ_CHECK_ARG(Sk == 0 || (k_packed && k_scales && v_packed && v_scales),
                 "kvq_decode_attn: null K/V pointer");
-  // Vector loads: 16-byte key chunks and 4-byte value dwords.
+  // Vector loads: 16-byte key chunks; 16-byte value pieces (matrix-core
+  // kernel) or 4-byte value dwords (VALU kernel); the matrix-core kernel loads
+  // a token's whole scale row (2, 4 or 8 bytes) at once.
+  const bool mfma = use_mfma(q_dtype, scale_dtype);
+  const int64_t v_align = mfma ? 16 : 4;
   const bool k_al = ((uintptr_t)k_packed % 16 == 0) && kp_strides[0] % 16 == 0 &&
                     kp_strides[1] % 16 == 0 && kp_strides[2] % 16 == 0;
-  const bool v_al = ((uintptr_t)v_packed % 4 == 0) && vp_strides[0] % 4 == 0 &&
-                    vp_strides[1] % 4 == 0 && vp_strides[2] % 4 == 0;
+  const bool v_al = ((uintptr_t)v_packed % v_align == 0) && vp_strides[0] % v_align == 0 &&
+                    vp_strides[1] % v_align == 0 && vp_strides[2] % v_align == 0;
   if (!k_al || !v_al) {
-    set_error("kvq_decode_attn: packed K rows must be 16-byte aligned and V rows 4-byte aligned");
+    set_error("kvq_decode_attn: packed K rows must be 16-byte aligned and V rows %lld-byte aligned",
+              (long long)v_align);
     return KVQ_EUNSUP;
+  }
+  if (mfma) {
+    const int64_t ng = (D + group_size - 1) / group_size;
+    const int64_t sz = ng >= 4 ? 8 : (ng == 2 ? 4 : 2);
+    bool s_al = true;
+    for (const int64_t* st : {ks_strides, vs_strides})
+      for (int i = 0; i < 3; ++i) s_al = s_al && (st[i] * 2) % sz == 0;
+    s_al = s_al && (uintptr_t)k_scales % sz == 0 && (uintptr_t)v_scales % sz == 0;
+    if (!s_al) {
+      set_error("kvq_decode_attn: scale rows must be %lld-byte aligned", (long long)sz);
+      return KVQ_EUNSUP;
+    }
   }
   // Token offsets inside one (batch, head) slice are 32-bit.
   if (Sk > 0 && (Sk * kp_strides[2] >= (1ll << 31) || Sk * vp_strides[2] >= (1ll << 31) ||
@@ -1162,7 +1282,6 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   a.row_chunks = p.row_chunks;
   a.n_units = p.n_units;
   a.n_split = p.n_split;
-  a.split_len = p.split_len;
   a.causal = is_causal ? 1 : 0;
   a.scale_dtype = scale_dtype;
   a.xcd_remap = (p.n_split > 1 && p.n_units % 8 == 0) ? 1 : 0;
@@ -1170,11 +1289,12 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   a.q_vec = (q_dtype != KVQ_F32 && q_strides[3] == 1 && (uintptr_t)q % 16 == 0 &&
              q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 && q_strides[2] % 8 == 0) ? 1 : 0;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  a.ws_ml = nullptr; a.ws_o = nullptr;
+  a.ws_cnt = nullptr; a.ws_ml = nullptr; a.ws_o = nullptr;
   if (need > 0) {
     char* w = (char*)workspace;
-    a.ws_ml = (float*)w;
-    a.ws_o = (float*)(w + ws_ml_bytes(p));
+    a.ws_cnt = (uint32_t*)w;
+    a.ws_ml = (float*)(w + ws_cnt_bytes(p));
+    a.ws_o = (float*)(w + ws_cnt_bytes(p) + ws_ml_bytes(p));
   }
   const bool rowmask = is_causal && Sq > 1;
   const dim3 grid((unsigned)((int64_t)p.n_units * p.n_split));
@@ -1182,21 +1302,5 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   if (D == 128) launch_d<128>(a, p, q_dtype, rowmask, grid, st);
   else launch_d<64>(a, p, q_dtype, rowmask, grid, st);
   KVQ_CHECK_LAUNCH("kvq_decode_attn");
-  if (p.n_split > 1) {
-    const int64_t threads = (int64_t)p.n_units * p.rows * D;
-    const dim3 mgrid((unsigned)((threads + 127) / 128));
-    switch (q_dtype) {
-      case KVQ_BF16:
-        hipLaunchKernelGGL(decode_attn_merge_kernel<KVQ_BF16>, mgrid, dim3(128), 0, st, a, p.rows, (int)D);
-        break;
-      case KVQ_F16:
-        hipLaunchKernelGGL(decode_attn_merge_kernel<KVQ_F16>, mgrid, dim3(128), 0, st, a, p.rows, (int)D);
-        break;
-      default:
-        hipLaunchKernelGGL(decode_attn_merge_kernel<KVQ_F32>, mgrid, dim3(128), 0, st, a, p.rows, (int)D);
-        break;
-    }
-    KVQ_CHECK_LAUNCH("kvq_decode_attn (split merge)");
-  }
   return KVQ_OK;
 }

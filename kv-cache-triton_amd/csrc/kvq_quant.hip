@@ -14,6 +14,8 @@
 // no cross-lane reduction is needed, and consecutive threads own consecutive
 // groups of the same row, which keeps the global accesses of a wave dense.
 
+#include <algorithm>
+
 #include "kvq_common.h"
 
 namespace kvq {
@@ -83,6 +85,82 @@ __global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
   store_from_f32(a.scales, sidx, a.scale_dtype, scale);
 }
 
+// ---------------------------------------------------------------------------
+// Vector path: one thread per 8-element chunk of a row (one 16-byte load for
+// 16-bit inputs, two for fp32), G/8 consecutive lanes per group. The group's
+// absmax is all-reduced across those lanes with DPP (quad xor 1, quad xor 2,
+// half-row mirror, row mirror), every lane divides its own 8 elements by the
+// group scale and packs them into one 4-byte store; the group's first lane
+// stores the scale. Taken when G is 8..128 (power of two), G divides D, x rows
+// have unit inner stride and 16-byte aligned starts, and packed rows are
+// 4-byte aligned; everything else takes quantize_kernel.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+
+template <int XDT, int LPG>  // LPG = lanes per group = G / 8
+__global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t cpr = a.D >> 3;  // chunks per row
+  const bool live = idx < a.rows * cpr;
+  const int64_t row = live ? idx / cpr : 0;
+  const int64_t ch = live ? idx - row * cpr : 0;
+  const int64_t s = row % a.S;
+  const int64_t bh = row / a.S;
+  const int64_t h = bh % a.H;
+  const int64_t b = bh / a.H;
+  const int64_t xoff = b * a.xs_b + h * a.xs_h + s * a.xs_s + 8 * ch;
+
+  float x[8];
+  if constexpr (XDT == KVQ_F32) {
+    const float4 lo = *(const float4*)((const float*)a.x + xoff);
+    const float4 hi = *(const float4*)((const float*)a.x + xoff + 4);
+    x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+    x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+  } else {
+    const uint4 w = *(const uint4*)((const uint16_t*)a.x + xoff);
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (XDT == KVQ_BF16) {
+        x[2 * j] = bf16_bits_to_f32(wd[j] & 0xffffu);
+        x[2 * j + 1] = bf16_bits_to_f32(wd[j] >> 16);
+      } else {
+        x[2 * j] = f16_bits_to_f32(wd[j] & 0xffffu);
+        x[2 * j + 1] = f16_bits_to_f32(wd[j] >> 16);
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+  // Every lane of the wave takes part in the DPP steps (dead lanes carry 0).
+  if constexpr (LPG >= 2) amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+  if constexpr (LPG >= 4) amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+  if constexpr (LPG >= 8) amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
+  if constexpr (LPG >= 16) amax = fmaxf(amax, dpp_f<0x140>(amax)); // row_mirror
+  if (!live) return;
+  // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
+  const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+  uint32_t word = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float qf = __builtin_rintf(x[e] / scale);  // round half to even
+    qf = fminf(fmaxf(qf, -8.0f), 7.0f);
+    word |= (uint32_t)((int)qf + 8) << (4 * e);
+  }
+  const int64_t pos = (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s;
+  // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
+  *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
+  if (ch % LPG == 0) {
+    const int64_t g = ch / LPG;
+    store_from_f32(a.scales, b * a.ss_b + h * a.ss_h + pos * a.ss_s + g, a.scale_dtype, scale);
+  }
+}
+
 struct DequantArgs {
   const uint8_t* packed;
   int64_t ps_b, ps_h, ps_s;
@@ -138,6 +216,8 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
   const int64_t ngroups = (D + group_size - 1) / group_size;
   if (rows == 0 || ngroups == 0) return KVQ_OK;
   KVQ_CHECK_ARG(x && packed && scales, "kvq_quantize: null data pointer");
+  KVQ_CHECK_ARG(rows * std::max<int64_t>(ngroups, (D + 7) / 8) / 256 < 0x7fffffffll,
+                "kvq_quantize: input too large for one launch");
 
   QuantArgs a;
   a.x = x;
@@ -151,10 +231,38 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
   a.write_pos = write_pos; a.write_pos0 = write_pos0;
   a.x_dtype = x_dtype; a.scale_dtype = scale_dtype;
 
+  hipStream_t st = (hipStream_t)stream;
+  const int lpg = (int)(group_size / 8);
+  const int64_t esz = dtype_size(x_dtype);
+  const bool vec = group_size % 8 == 0 && group_size <= 128 && (lpg & (lpg - 1)) == 0 &&
+                   D % group_size == 0 && a.xs_d == 1 &&
+                   (uintptr_t)x % 16 == 0 && (a.xs_b * esz) % 16 == 0 && (a.xs_h * esz) % 16 == 0 &&
+                   (a.xs_s * esz) % 16 == 0 &&
+                   (uintptr_t)packed % 4 == 0 && a.ps_b % 4 == 0 && a.ps_h % 4 == 0 && a.ps_s % 4 == 0;
+  if (vec) {
+    const int64_t total = rows * (D / 8);
+    const dim3 grid((unsigned)((total + 255) / 256));
+#define KVQ_QVEC(XDT)                                                                              \
+    switch (lpg) {                                                                                 \
+      case 1: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 1>), grid, dim3(256), 0, st, a); break;   \
+      case 2: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 2>), grid, dim3(256), 0, st, a); break;   \
+      case 4: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 4>), grid, dim3(256), 0, st, a); break;   \
+      case 8: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 8>), grid, dim3(256), 0, st, a); break;   \
+      default: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 16>), grid, dim3(256), 0, st, a); break; \
+    }
+    switch (x_dtype) {
+      case KVQ_BF16: KVQ_QVEC(KVQ_BF16) break;
+      case KVQ_F16: KVQ_QVEC(KVQ_F16) break;
+      default: KVQ_QVEC(KVQ_F32) break;
+    }
+#undef KVQ_QVEC
+    KVQ_CHECK_LAUNCH("kvq_quantize");
+    return KVQ_OK;
+  }
+
   const int64_t total = rows * ngroups;
   const dim3 block(256);
   const dim3 grid((unsigned)((total + 255) / 256));
-  hipStream_t st = (hipStream_t)stream;
   switch (x_dtype) {
     case KVQ_BF16: hipLaunchKernelGGL(quantize_kernel<KVQ_BF16>, grid, block, 0, st, a); break;
     case KVQ_F16: hipLaunchKernelGGL(quantize_kernel<KVQ_F16>, grid, block, 0, st, a); break;

@@ -42,8 +42,9 @@ def test_num_splits_planning():
     B16, F16, F32 = nat.KVQ_BF16, nat.KVQ_F16, nat.KVQ_F32
     # Llama-3.1-8B decode at 16K on 256 CUs: 8 KV heads x 32 splits (512 tokens each)
     assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 16384, B16, B16, 256) == 32
-    # never more splits than one 64-token tile per wave (4 waves)
-    assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 600, B16, B16, 256) == 3
+    # no split shorter than two 64-token tiles
+    assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 600, B16, B16, 256) == 4
+    assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 100, B16, B16, 256) == 1
     # plenty of units already -> one split
     assert lib.kvq_decode_attn_num_splits(16, 25, 25, 1, 64, 1024, F16, F16, 256) == 1
     # fp32 queries plan for the VALU kernel (32-token tiles at D=64)
@@ -57,7 +58,7 @@ def test_workspace_bytes():
     B16 = nat.KVQ_BF16
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 1) == 0
     ws = lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 32)
-    # 8 units x 32 splits x 4 rows x (128 + 2) floats, plus an aligned counter block
+    # 8 units x 32 splits x 4 rows x (128 + 2) floats, plus 256-byte counter and padding blocks
     assert ws >= 8 * 32 * 4 * 130 * 4 and ws < 8 * 32 * 4 * 130 * 4 + 1024
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, 7, B16, 4) == nat.KVQ_EINVAL
 
