@@ -114,6 +114,26 @@ __device__ __forceinline__ float dpp(float v, float old) {
                                                                ROW_MASK, 0xF, false));
 }
 
+// Lane swaps of gfx950: permlane32 exchanges lanes 32-63 of `x` with lanes
+// 0-31 of `y`; permlane16 exchanges the odd 16-lane rows of `x` with the even
+// rows of `y`. The two results are read out of the builtin's two-element
+// vector by value (a bit cast applied directly to an element of it reads
+// element 0 with this toolchain).
+__device__ __forceinline__ void permlane32_swap(float& x, float& y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, y), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  x = __builtin_bit_cast(float, r0);
+  y = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void permlane16_swap(float& x, float& y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, y), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  x = __builtin_bit_cast(float, r0);
+  y = __builtin_bit_cast(float, r1);
+}
+
 // Full-wave reductions; the result is read from lane 63 and is wave-uniform.
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0x111>(v, kNeg));  // row_shr:1
@@ -168,79 +188,135 @@ __device__ __forceinline__ int64_t out_index(const AttnArgs& a, int b, int kvh, 
 }
 
 // Token range [t0, t1) of split `split` over a sequence of L keys.
+// 32-bit arithmetic: the host keeps Sk * kMaxSplit below 2^32.
 __device__ __forceinline__ void split_range(const AttnArgs& a, int L, int split, int& t0, int& t1) {
-  t0 = (int)(((int64_t)split * L) / a.n_split);
-  t1 = (int)(((int64_t)(split + 1) * L) / a.n_split);
+  const uint32_t ns = (uint32_t)a.n_split;
+  t0 = (int)(((uint32_t)split * (uint32_t)L) / ns);
+  t1 = (int)(((uint32_t)(split + 1) * (uint32_t)L) / ns);
 }
 
 constexpr int kMaxRows = 8;  // query rows per workgroup (both kernels)
+
+// Buffer descriptor over `bytes` bytes at p (raw, 32-bit data format): loads
+// at offsets >= bytes return zero and touch no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct MergeLds {
   float l[kMaxRows];
   float m[kMaxRows];
   float wf[8][kMaxRows];           // per-wave rescale factors 2^(m_wave - M)
   int last;                        // this workgroup merges the unit's splits
+  // cross-split merge (last workgroup only)
+  float2 ml[kMaxSplit * kMaxRows];  // (max, sum) per (split, row)
+  float sw[kMaxRows][kMaxSplit];    // 2^(m_split - M) per (row, split)
+  float sl[kMaxRows];               // merged denominators
+  float4 part[512];                 // per-thread partial sums of 4 dims
 };
 
 // Partials cross between workgroups that may sit on different XCDs (each with
-// its own L2), so they are written and read with device-scope accesses (the
-// sc1 cache policy: stores write through to the device-coherent level, loads
-// do not hit a stale L2 copy). That needs no L2 writeback or invalidate, which
-// a device-scope fence would issue.
-__device__ __forceinline__ void ws_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ws_load(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// its own L2), so they are written and read with the device-scope cache
+// policy (sc1: stores write through to the device-coherent level, loads do
+// not hit a stale L2 copy). That needs no L2 writeback or invalidate, which a
+// device-scope fence would issue.
+constexpr int kSc1 = 16;  // cache-policy bits of a buffer access: SC1 (device scope)
+
+// Bits -> float through a by-value parameter. (This toolchain's
+// __builtin_bit_cast applied directly to a vector element such as v.y reads
+// element 0 whatever the element named.)
+__device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 
 // Cross-split merge, run by the last workgroup of a unit to finish: out =
-// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. Each
-// thread owns (row, dim) outputs and issues the loads of all partials it needs
-// (the row's (max, sum) pairs and its o values, BATCH splits at a time) before
-// using any of them, so the merge costs one round trip per BATCH splits. A row
-// no split saw a key for (all l_s = 0) yields zeros.
+// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. The unit's
+// partial rows o[split][row][D] are read as 16-byte pieces spread over every
+// thread — thread t owns dims 4 (t % (D/4)) .. +4 of row (t / (D/4)) % ROWS of
+// the splits congruent to t / (ROWS*D/4) — issued together with the (max, sum)
+// pairs before any is used. One wave per row turns the pairs into per-split
+// factors (lane = split), threads fold their splits, and the groups of
+// threads sharing a (row, 4 dims) are summed through LDS. A row no split saw a
+// key for (all l_s = 0) yields zeros.
 template <int ROWS, int D, int OUT_DT, int NW>
-__device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc, int kvh, int b) {
+__device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc, int kvh, int b,
+                                             MergeLds& mg) {
   constexpr int NT = 64 * NW;
-  constexpr int BATCH = 32;
+  constexpr int Q = ROWS * D / 4;  // 16-byte pieces per split
+  static_assert(Q <= NT && NT % Q == 0, "merge mapping");
+  constexpr int P = NT / Q;         // thread groups per piece
+  constexpr int BATCH = 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ns = a.n_split;
+  const int piece = tid % Q, grp = tid / Q;
+  const int r = piece / (D / 4), d4 = piece % (D / 4);
   const int64_t slot0 = (int64_t)unit * ns * ROWS;  // + split * ROWS + row
-  for (int idx = threadIdx.x; idx < ROWS * D; idx += NT) {
-    const int r = idx / D, d = idx % D;
-    const float* mlb = a.ws_ml + 2 * (slot0 + r);
-    const float* ob = a.ws_o + (slot0 + r) * D + d;
-    const int64_t ml_step = 2 * ROWS, o_step = (int64_t)ROWS * D;
-    float M = kNeg, Ls = 0.0f, acc = 0.0f;
-    for (int sp0 = 0; sp0 < ns; sp0 += BATCH) {
-      float mv[BATCH], lv[BATCH], ov[BATCH];
+  const __amdgpu_buffer_rsrc_t ro =
+      buffer_rsrc(a.ws_o + slot0 * D, (uint32_t)((int64_t)ns * ROWS * D * 4));
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.ws_ml + slot0 * 2, (uint32_t)(ns * ROWS * 8));
+  const int nj = (ns - grp + P - 1) / P;  // splits grp, grp + P, ... < ns
+  // issue the first BATCH pieces and the pairs before using anything
+  u32x4_t ov[BATCH];
+#pragma unroll
+  for (int j = 0; j < BATCH; ++j) {
+    const uint32_t sp = (uint32_t)(grp + P * j);
+    ov[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                            ro, (sp * Q + piece) * 16u, 0, kSc1));  // past ns: zeros
+  }
+  for (int i = tid; i < ns * ROWS; i += NT) {
+    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rm, 8u * i, 0, kSc1));
+    mg.ml[i] = make_float2(u32_as_f32(v.x), u32_as_f32(v.y));
+  }
+  __syncthreads();
+  for (int rr = wave; rr < ROWS; rr += NW) {
+    const bool on = lane < ns;
+    const float2 ml = on ? mg.ml[lane * ROWS + rr] : make_float2(kNeg, 0.0f);
+    const float M = wave_max(ml.x);
+    const float w = on ? __builtin_amdgcn_exp2f(ml.x - M) : 0.0f;
+    const float Ls = wave_sum(ml.y * w);
+    if (on) mg.sw[rr][lane] = w;
+    if (lane == 0) mg.sl[rr] = Ls;
+  }
+  __syncthreads();
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int j0 = 0; j0 < nj; j0 += BATCH) {
+    if (j0 > 0) {
 #pragma unroll
       for (int j = 0; j < BATCH; ++j) {
-        const int64_t sp = min(sp0 + j, ns - 1);
-        mv[j] = ws_load(mlb + sp * ml_step);
-        lv[j] = ws_load(mlb + sp * ml_step + 1);
-        ov[j] = ws_load(ob + sp * o_step);
-      }
-      float Mb = M;
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j)
-        if (sp0 + j < ns) Mb = fmaxf(Mb, mv[j]);
-      const float f = __builtin_amdgcn_exp2f(M - Mb);
-      Ls *= f;
-      acc *= f;
-      M = Mb;
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        if (sp0 + j < ns) {
-          const float w = __builtin_amdgcn_exp2f(mv[j] - M);
-          Ls = fmaf(lv[j], w, Ls);
-          acc = fmaf(ov[j], w, acc);
-        }
+        const uint32_t sp = (uint32_t)(grp + P * (j0 + j));
+        ov[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                ro, (sp * Q + piece) * 16u, 0, kSc1));
       }
     }
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      if (j0 + j < nj) {
+        const float w = mg.sw[r][grp + P * (j0 + j)];
+        acc.x = fmaf(u32_as_f32(ov[j].x), w, acc.x);
+        acc.y = fmaf(u32_as_f32(ov[j].y), w, acc.y);
+        acc.z = fmaf(u32_as_f32(ov[j].z), w, acc.z);
+        acc.w = fmaf(u32_as_f32(ov[j].w), w, acc.w);
+      }
+    }
+  }
+  mg.part[tid] = acc;
+  __syncthreads();
+  if (tid < Q) {
+    float4 s = mg.part[tid];
+#pragma unroll
+    for (int g = 1; g < P; ++g) {
+      const float4 o = mg.part[tid + g * Q];
+      s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
+    }
     const int rho = rc * ROWS + r;
-    if (rho < a.rows_total)
-      store_from_f32(a.out, out_index(a, b, kvh, rho, d), OUT_DT, Ls > 0.0f ? acc / Ls : 0.0f);
+    const float Ls = mg.sl[r];
+    if (rho < a.rows_total) {
+      const float o4[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        store_from_f32(a.out, out_index(a, b, kvh, rho, 4 * d4 + k), OUT_DT, Ls > 0.0f ? o4[k] / Ls : 0.0f);
+    }
   }
 }
 
@@ -286,10 +362,10 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
         store_from_f32(a.out, out_index(a, b, kvh, rho, d), OUT_DT, Ls > 0.0f ? Os / Ls : 0.0f);
     } else {
       const int64_t slot = ((int64_t)unit * a.n_split + split) * ROWS + r;
-      ws_store(a.ws_o + slot * D + d, Os);
+      __hip_atomic_store(a.ws_o + slot * D + d, Os, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == 0) {
-        ws_store(a.ws_ml + slot * 2 + 0, mg.m[r]);
-        ws_store(a.ws_ml + slot * 2 + 1, Ls);
+        __hip_atomic_store(a.ws_ml + slot * 2 + 0, mg.m[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ws_ml + slot * 2 + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -303,7 +379,7 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
   }
   __syncthreads();
   if (!mg.last) return;
-  merge_splits<ROWS, D, OUT_DT, NW>(a, unit, rc, kvh, b);
+  merge_splits<ROWS, D, OUT_DT, NW>(a, unit, rc, kvh, b, mg);
   if (tid == 0) __hip_atomic_store(a.ws_cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
@@ -318,18 +394,11 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
 // 1024 + n). Key dword k therefore feeds the MFMA k-order (0,2,1,3) and
 // (4,6,5,7); the staged query rows are permuted the same way.
 
-// Buffer descriptor over `bytes` bytes at p (raw, 32-bit data format): loads
-// at offsets >= bytes return zero and touch no memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
-                                           0x00020000);
-}
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-template <int D, int RS, int QM, bool ROWMASK, int NW, int CH>
+template <int D, int RS, int QM, int SM, bool ROWMASK, int NW, int CH>
 __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArgs a) {
   constexpr bool F16 = QM == KVQ_F16;
+  constexpr bool S_F16 = SM == KVQ_F16;
   constexpr int LPT = D / 32;       // 32-dim chunks (16 code bytes) per token
   constexpr int VROW = D / 2;       // code bytes per token row
   constexpr int VLD = VROW * 64 / 1024;  // 16-byte V loads per lane per 64-token tile
@@ -346,19 +415,26 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   static_assert(QT <= 64 * NW, "query staging");
 
   // Per wave: the V codes of the tile being consumed (row-major image of the
-  // tile, 64 x VROW bytes) and its softmax weights [rowset][row][chunk]
-  // [subtile][tsub][4 tokens]. Once the sequence loop is done the same bytes
-  // hold the per-wave partial outputs.
+  // tile, 64 x VROW bytes) and its softmax weights, [rowset][subtile] blocks of
+  // 4 * LPT * VTS * 4 bf16 in which (row, chunk) pair rc = 4 * chunk + row,
+  // token subset ts and position k sit at ((rc ^ subtile) * VTS + ts) * 4 + k:
+  // a PV read (one subtile, every (rc, ts)) covers one contiguous block and a
+  // token-lane write (one rc, every token) spreads its subtiles over distinct
+  // banks. Once the sequence loop is done the same bytes hold the per-wave
+  // partial outputs.
   constexpr int V_BYTES = NW * 64 * VROW;
   constexpr int W_BYTES = NW * RS * 4 * LPT * NSUB * VTS * 4 * 2;
   constexpr int O_BYTES = NW * ROWS * D * 4;
   constexpr int S_BYTES = V_BYTES + W_BYTES > O_BYTES ? V_BYTES + W_BYTES : O_BYTES;
-  __shared__ __attribute__((aligned(16))) uint32_t q_lds[ROWS][D / 2];
+  // query rows padded by 16 bytes so the four rows a QK read touches sit in
+  // different LDS banks
+  constexpr int QROW = D / 2 + 4;
+  __shared__ __attribute__((aligned(16))) uint32_t q_lds[ROWS][QROW];
   __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
   __shared__ float ml_lds[NW][ROWS][2];
   __shared__ MergeLds mg;
   auto v_lds = reinterpret_cast<uint8_t(*)[64 * VROW]>(smem);
-  auto w_lds = reinterpret_cast<uint16_t(*)[RS][4][LPT][NSUB][VTS][4]>(smem + V_BYTES);
+  auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem + V_BYTES);
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
   const int tid = threadIdx.x;
@@ -393,7 +469,6 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const __amdgpu_buffer_rsrc_t rks = buffer_rsrc(ks_bh, Le * kss2);
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vp_bh, Le * vps);
   const __amdgpu_buffer_rsrc_t rvs = buffer_rsrc(vs_bh, Le * vss2);
-  const bool s_f16 = a.scale_dtype == KVQ_F16;
   const int ng = (D + a.G - 1) / a.G;  // scales per token row: 1, 2 or 4 (wave-uniform)
   uint32_t gsh[LPT];  // bit offset of each 32-dim chunk's scale in the loaded scale row
 #pragma unroll
@@ -402,8 +477,8 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   // PV lane layout and the LDS slot this lane's token fills
   const int vts = lane / VLPT;
   const int vj = lane % VLPT;
-  const int v_row = vj & 3;   // A-operand row of this lane's block
-  const int v_chunk = vj >> 2;
+  const int v_rc = vj;                      // A-operand (row, chunk) of this lane's block:
+                                            // row vj & 3, chunk vj >> 2, i.e. rc = vj
   const int w_sub = lane / SUB;             // sub-tile of token `lane`
   const int w_ts = (lane % SUB) % VTS;      // its token subset
   const int w_k = (lane % SUB) / VTS;       // its position in the subset
@@ -446,12 +521,39 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       vq[i][j] = __builtin_bit_cast(u32x4_t,
                                     __builtin_amdgcn_raw_buffer_load_b128(rv, (t0 + v_tok[j]) * vps + v_off[j], 0, 0));
   };
+  // ---- query loads go out first (threads < QT; thread (q_r, q_k) reads
+  //      elements [8 q_k, 8 q_k + 8) of row q_r; rows past the last one read
+  //      row 0 and are zeroed) ----
+  const int q_r = tid / (D / 8), q_k = tid % (D / 8);
+  const bool q_ok = rc * ROWS + q_r < a.rows_total;
+  uint4 qraw = make_uint4(0u, 0u, 0u, 0u);  // elements (e0,e1) (e2,e3) (e4,e5) (e6,e7)
+  if (tid < QT) {
+    const int rho = q_ok ? rc * ROWS + q_r : 0;
+    const int head = kvh * a.ratio + rho / a.Sq, qi = rho % a.Sq;
+    const int64_t qoff = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
+                         (int64_t)(8 * q_k) * a.qs_d;
+    if (a.q_vec) {
+      qraw = *(const uint4*)((const uint16_t*)a.q + qoff);  // used only after the cache loads
+    } else {
+      const uint16_t* q16 = (const uint16_t*)a.q + qoff;
+      uint32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = q16[(int64_t)j * a.qs_d];
+      qraw = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+    }
+  }
+
   // With one row set the first chunk's loads go out before the query is
-  // staged; two row sets load each chunk at the top of the loop.
+  // staged; two row sets load each chunk at the top of the loop. Tile 0's
+  // loads are unconditional (a wave without a tile reads past the split's
+  // end: zeros, no memory traffic), which keeps the compiler's wait for the
+  // query exact.
   constexpr bool PIPE = RS == 1;
   if constexpr (PIPE) {
+    load_k(0, wave);
+    load_v(0, wave);
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
+    for (int i = 1; i < CH; ++i) {
       if (wave + NW * i < ntiles) {
         load_k(i, wave);
         load_v(i, wave);
@@ -459,34 +561,12 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     }
   }
 
-  // ---- query rows -> LDS, permuted to the key operand order: thread (q_r,
-  //      q_k) < QT stages elements [8 q_k, 8 q_k + 8) of row q_r; rows past
-  //      the last one are zeros ----
+  // ---- query rows -> LDS, permuted to the key operand order ----
   if (tid < QT) {
-    const int q_r = tid / (D / 8), q_k = tid % (D / 8);
-    const int q_rho = rc * ROWS + q_r;
-    const bool q_ok = q_rho < a.rows_total;
-    const int rho = q_ok ? q_rho : 0;
-    const int head = kvh * a.ratio + rho / a.Sq, qi = rho % a.Sq;
-    const int64_t qoff = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
-                         (int64_t)(8 * q_k) * a.qs_d;
-    uint32_t qe[8];
-    if (a.q_vec) {
-      const uint4 w = *(const uint4*)((const uint16_t*)a.q + qoff);
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        qe[2 * j] = wd[j] & 0xffffu;
-        qe[2 * j + 1] = wd[j] >> 16;
-      }
-    } else {
-      const uint16_t* q16 = (const uint16_t*)a.q + qoff;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qe[j] = q16[(int64_t)j * a.qs_d];
-    }
-    const uint32_t keep = q_ok ? 0xffffu : 0u;
-    const u32x4_t qp = {(qe[0] & keep) | ((qe[2] & keep) << 16), (qe[1] & keep) | ((qe[3] & keep) << 16),
-                        (qe[4] & keep) | ((qe[6] & keep) << 16), (qe[5] & keep) | ((qe[7] & keep) << 16)};
+    const uint32_t keep = q_ok ? 0xffffffffu : 0u;
+    const uint32_t x = qraw.x & keep, y = qraw.y & keep, z = qraw.z & keep, w = qraw.w & keep;
+    const u32x4_t qp = {__builtin_amdgcn_perm(y, x, 0x05040100u), __builtin_amdgcn_perm(y, x, 0x07060302u),
+                        __builtin_amdgcn_perm(w, z, 0x05040100u), __builtin_amdgcn_perm(w, z, 0x07060302u)};
     *(u32x4_t*)&q_lds[q_r][4 * q_k] = qp;  // (e0,e2) (e1,e3) (e4,e6) (e5,e7)
   }
   __syncthreads();
@@ -581,7 +661,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
         float skl[LPT];
 #pragma unroll
         for (int c = 0; c < LPT; ++c)
-          skl[c] = scale16_to_f32((uint32_t)(skw >> gsh[c]) & 0xffffu, s_f16) * a.scale_log2;
+          skl[c] = scale16_to_f32((uint32_t)(skw >> gsh[c]) & 0xffffu, S_F16) * a.scale_log2;
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
@@ -633,7 +713,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
         const uint64_t svw = ((uint64_t)svr[i].y << 32) | svr[i].x;
         float svl[LPT];
 #pragma unroll
-        for (int c = 0; c < LPT; ++c) svl[c] = scale16_to_f32((uint32_t)(svw >> gsh[c]) & 0xffffu, s_f16);
+        for (int c = 0; c < LPT; ++c) svl[c] = scale16_to_f32((uint32_t)(svw >> gsh[c]) & 0xffffu, S_F16);
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
@@ -643,7 +723,8 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
             l_acc[rs][r] += p;
 #pragma unroll
             for (int c = 0; c < LPT; ++c)
-              w_lds[wave][rs][r][c][w_sub][w_ts][w_k] = __builtin_bit_cast(uint16_t, (__bf16)(p * svl[c]));
+              w_lds[wave][rs][w_sub][(((4 * c + r) ^ w_sub) * VTS + w_ts) * 4 + w_k] =
+                  __builtin_bit_cast(uint16_t, (__bf16)(p * svl[c]));
           }
         }
       }
@@ -677,7 +758,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
         }
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
-          const uint2 wa = *(const uint2*)&w_lds[wave][rs][v_row][v_chunk][s][vts][0];
+          const uint2 wa = *(const uint2*)&w_lds[wave][rs][s][((v_rc ^ s) * VTS + vts) * 4];
 #pragma unroll
           for (int m = 0; m < 8; ++m)
             o_acc[rs][m] = mfma4<false>(wa.x, wa.y, bp[0][m], bp[1][m], o_acc[rs][m]);
@@ -690,39 +771,69 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     }
   }
 
-  // ---- wave partial: sum over the VTS token subsets (lanes VLPT apart),
-  //      then o[row][8*vj + m] -> LDS (over the V/weight bytes, so every wave
-  //      must be done with those first) ----
-  float ov[RS][4][8];
-#pragma unroll
-  for (int rs = 0; rs < RS; ++rs) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        float v = fmaf(-136.0f, w_acc[rs][r], o_acc[rs][m][r]);
-#pragma unroll
-        for (int step = VLPT; step < 64; step *= 2) v += __shfl_xor(v, step, 64);
-        ov[rs][r][m] = v;
-      }
-    }
-  }
-  float lsum[RS][4];
+  // ---- wave partial: the N = 32 * RS values of a lane (row rho = idx / 8,
+  //      dim 8 vj + idx % 8, idx = 8 * rho + m) summed over the VTS token
+  //      subsets (lanes VLPT apart) by swap-and-halve steps: each step pairs
+  //      value i with value i + n/2 across lanes 32 (permlane32 swap), 16
+  //      (permlane16 swap) or 8 (row rotate, D = 64) apart, and each lane keeps
+  //      the half its side of the pair owns. Afterwards the lane of subset g
+  //      holds values [g * N / VTS, (g + 1) * N / VTS). Then -> LDS (over the
+  //      V/weight bytes, so every wave must be done with those). ----
+  constexpr int NV = 32 * RS;
+  float val[NV];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) lsum[rs][r] = wave_sum(l_acc[rs][r]);
-  __syncthreads();
-  if (vts == 0) {
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int rs = 0; rs < RS; ++rs) {
+      for (int m = 0; m < 8; ++m)
+        val[(rs * 4 + r) * 8 + m] = fmaf(-136.0f, w_acc[rs][r], o_acc[rs][m][r]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float* dst = &o_lds[wave][rs * 4 + r][8 * vj];
-        *(float4*)dst = make_float4(ov[rs][r][0], ov[rs][r][1], ov[rs][r][2], ov[rs][r][3]);
-        *(float4*)(dst + 4) = make_float4(ov[rs][r][4], ov[rs][r][5], ov[rs][r][6], ov[rs][r][7]);
-      }
+  for (int i = 0; i < NV / 2; ++i) {
+    float x = val[i], y = val[i + NV / 2];
+    permlane32_swap(x, y);
+    val[i] = x + y;
+  }
+#pragma unroll
+  for (int i = 0; i < NV / 4; ++i) {
+    float x = val[i], y = val[i + NV / 4];
+    permlane16_swap(x, y);
+    val[i] = x + y;
+  }
+  if constexpr (VTS == 8) {
+    const bool hi8 = (lane & 8) != 0;
+#pragma unroll
+    for (int i = 0; i < NV / 8; ++i) {
+      const float send = hi8 ? val[i] : val[i + NV / 8];
+      const float keep = hi8 ? val[i + NV / 8] : val[i];
+      val[i] = keep + dpp<0x128>(send, 0.0f);  // row_ror:8 = the lane 8 apart
     }
+  }
+  constexpr int NK = NV / VTS;  // values a lane keeps
+  // row sums of the softmax denominators: rows 0-3 of each row set land in
+  // lane groups 0-3 after the two swaps, then a 16-lane row reduction
+  float lsum[RS][4];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) {
+    float l0 = l_acc[rs][0], l2 = l_acc[rs][2], l1 = l_acc[rs][1], l3 = l_acc[rs][3];
+    permlane32_swap(l0, l2);
+    permlane32_swap(l1, l3);
+    float x = l0 + l2, y = l1 + l3;
+    permlane16_swap(x, y);
+    float v = x + y;
+    v += dpp<0x111>(v, 0.0f);  // row_shr:1
+    v += dpp<0x112>(v, 0.0f);  // row_shr:2
+    v += dpp<0x114>(v, 0.0f);  // row_shr:4
+    v += dpp<0x118>(v, 0.0f);  // row_shr:8 -> lane 15 of each row holds the row's total
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      lsum[rs][r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r + 15));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NK; i += 4) {
+    const int idx = NK * vts + i;  // first of 4 consecutive values (same row)
+    *(float4*)&o_lds[wave][idx / 8][8 * vj + idx % 8] = make_float4(val[i], val[i + 1], val[i + 2], val[i + 3]);
   }
   if (lane == 0) {
 #pragma unroll
@@ -1093,18 +1204,23 @@ template <int RS>
 constexpr int mfma_waves() { return RS == 1 ? 8 : 4; }
 constexpr int kMfmaTilesInFlight = 2;
 
-template <int D, int RS, int QM>
+template <int D, int RS, int QM, int SM>
 static void launch_mfma_rs(const AttnArgs& a, bool rowmask, dim3 grid, hipStream_t st) {
   constexpr int NW = mfma_waves<RS>();
   constexpr int CH = kMfmaTilesInFlight;
-  if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, true, NW, CH>), grid, dim3(64 * NW), 0, st, a);
-  else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, false, NW, CH>), grid, dim3(64 * NW), 0, st, a);
+  if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, true, NW, CH>), grid, dim3(64 * NW), 0, st, a);
+  else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, false, NW, CH>), grid, dim3(64 * NW), 0, st, a);
 }
 
 template <int D, int QM>
 static void launch_mfma(const AttnArgs& a, int rows, bool rowmask, dim3 grid, hipStream_t st) {
-  if (rows <= 4) launch_mfma_rs<D, 1, QM>(a, rowmask, grid, st);
-  else launch_mfma_rs<D, 2, QM>(a, rowmask, grid, st);
+  if (a.scale_dtype == KVQ_F16) {
+    if (rows <= 4) launch_mfma_rs<D, 1, QM, KVQ_F16>(a, rowmask, grid, st);
+    else launch_mfma_rs<D, 2, QM, KVQ_F16>(a, rowmask, grid, st);
+  } else {
+    if (rows <= 4) launch_mfma_rs<D, 1, QM, KVQ_BF16>(a, rowmask, grid, st);
+    else launch_mfma_rs<D, 2, QM, KVQ_BF16>(a, rowmask, grid, st);
+  }
 }
 
 template <int D, int ROWS, int QM>
@@ -1247,7 +1363,7 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
     set_error("kvq_decode_attn: a (batch, head) slice of the cache exceeds 2 GiB");
     return KVQ_EUNSUP;
   }
-  KVQ_CHECK_ARG(Sk <= 0x7fffffffll && Sq <= 0x7fffffffll, "kvq_decode_attn: sequence too long");
+  KVQ_CHECK_ARG(Sk * kMaxSplit < (1ll << 32) && Sq <= 0x7fffffffll, "kvq_decode_attn: sequence too long");
 
   Plan p;
   const int rc = make_plan(B, Hq, Hkv, Sq, D, Sk, q_dtype, scale_dtype, n_split, 1, &p);
