@@ -80,7 +80,25 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed region, run a plain device copy of this many MiB (the "
+                         "calibration kernel for rocprof FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic-summary", default=os.path.join(ROOT, "profiles", "decode_attn_llama8b_16k_traffic.txt"),
+                    help="rocprof counter summary to take roofline.traffic from (if it covers this workload)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no GPU work: turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE run, "
+                         "WRITE_SIZE run of this script with --calib-copy-mib) into a traffic summary on stdout")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
+                    help="no GPU work: turn a rocprofv3 --kernel-trace --stats kernel_stats.csv into a summary")
+    ap.add_argument("--cmd", default="", help="command line recorded in a summary")
     args = ap.parse_args()
+
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.calib_copy_mib, args.cmd))
+        return 0
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.cmd))
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); the INT4 decode "
@@ -218,6 +236,20 @@ def main() -> int:
             print("bench.py: attention-only graph replay differs from the eager step", file=sys.stderr)
             return 1
 
+    if args.calib_copy_mib:
+        # an elementwise kernel that reads n bytes and writes n bytes (bitwise
+        # not of uint8; a same-dtype copy_ would go to a DMA engine, which kernel
+        # counters do not see): the reference point that scales rocprof's
+        # FETCH_SIZE / WRITE_SIZE readings to bytes
+        n = args.calib_copy_mib << 20
+        src_buf = torch.zeros(n, dtype=torch.uint8, device=dev)
+        dst_buf = torch.empty_like(src_buf)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                torch.bitwise_not(src_buf, out=dst_buf)
+        torch.cuda.synchronize()
+        del src_buf, dst_buf
+
     kv_tokens = int((seq_lens + 1).sum().item()) if seq_lens is not None else B * attended
     a_bytes = attn_bytes(w, kv_tokens)
     step_bytes = L * (a_bytes + append_bytes(w))
@@ -251,8 +283,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_attn_kernel",
+            "traffic": read_traffic(args.traffic_summary, w),
+            "kernel": "decode_attn_mfma_kernel" if w["dtype"] != "f32" else "decode_attn_valu_kernel",
             "bytes_per_launch": a_bytes,
         },
     }
@@ -261,6 +293,91 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(w, layers, attended, seq_lens, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def _counter_medians(path: str) -> dict:
+    """Median per (kernel name, counter) of a rocprofv3 counter_collection.csv."""
+    import csv
+    import statistics
+
+    vals: dict = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], row["Counter_Name"])
+            vals.setdefault(key, []).append(float(row["Counter_Value"]))
+    return {k: (statistics.median(v), len(v)) for k, v in vals.items()}
+
+
+def _pick(med: dict, counter: str, want) -> tuple:
+    """(kernel name, median, dispatches) of the kernel matching `want` with the
+    largest median reading of `counter`."""
+    best = None
+    for (name, cname), (m, n) in med.items():
+        if cname == counter and want(name) and (best is None or m > best[1]):
+            best = (name, m, n)
+    if best is None:
+        raise SystemExit(f"no kernel with counter {counter} matched in the summary input")
+    return best
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, calib_mib: int, cmd: str) -> str:
+    """Traffic summary: the attention kernel's FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch, median over dispatches), each scaled by expected / measured of the
+    same counter on the calibration kernel (bitwise not over calib_mib MiB, which
+    reads and writes calib_mib MiB)."""
+    if calib_mib <= 0:
+        raise SystemExit("--summarize-pmc needs --calib-copy-mib (the size the profiled run copied)")
+    is_attn = lambda n: "decode_attn_" in n and "merge" not in n
+    is_copy = lambda n: "bitwise_not" in n
+    out = []
+    res = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        med = _counter_medians(path)
+        an, av, ad = _pick(med, counter, is_attn)
+        cn, cv, cd = _pick(med, counter, is_copy)
+        expect_kib = calib_mib * 1024.0
+        factor = expect_kib / cv if cv > 0 else float("nan")
+        res[counter] = av * factor
+        out.append(f"{counter}: attention {av:.1f} KiB/dispatch (median of {ad}; {an[:80]})")
+        out.append(f"{counter}: calibration copy {cv:.1f} KiB/dispatch for {expect_kib:.0f} KiB moved "
+                   f"(median of {cd}; {cn[:80]}) -> factor {factor:.4f}")
+    total = (res["FETCH_SIZE"] + res["WRITE_SIZE"]) * 1024.0
+    out.append(f"traffic_bytes_per_launch: {total:.0f}")
+    out.append(f"fetch_bytes_per_launch: {res['FETCH_SIZE'] * 1024.0:.0f}")
+    out.append(f"write_bytes_per_launch: {res['WRITE_SIZE'] * 1024.0:.0f}")
+    return "\n".join([f"command: {cmd}" if cmd else "command: (not recorded)"] + out)
+
+
+def summarize_trace(stats_csv: str, cmd: str) -> str:
+    """Per-kernel call count and average / min / max duration from a rocprofv3
+    --stats kernel_stats.csv, kvq kernels first."""
+    import csv
+
+    rows = list(csv.DictReader(open(stats_csv)))
+    rows.sort(key=lambda r: ("kvq::" not in r["Name"], -float(r["TotalDurationNs"])))
+    out = [f"command: {cmd}" if cmd else "command: (not recorded)",
+           f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}  kernel"]
+    for r in rows[:12]:
+        out.append(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.3f} {float(r['MinNs']) / 1e3:9.3f} "
+                   f"{float(r['MaxNs']) / 1e3:9.3f} {float(r['Percentage']):6.2f}  {r['Name'][:110]}")
+    return "\n".join(out)
+
+
+def read_traffic(path: str, w: dict):
+    """traffic_bytes_per_launch from a committed summary, if it was made for
+    this workload (its command names the same --workload and no other context)."""
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    cmd = next((l for l in text.splitlines() if l.startswith("command:")), "")
+    wl = "ns" if "--workload" not in cmd else cmd.split("--workload", 1)[1].split()[0]
+    if WORKLOADS.get(wl, {}).get("desc") != w["desc"] or "--ctx" in cmd:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def cpu_baseline(w: dict, layers: list, attended: int, seq_lens, budget_s: float) -> dict:
