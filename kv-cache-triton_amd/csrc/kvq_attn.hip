@@ -207,15 +207,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct MergeLds {
-  float l[kMaxRows];
-  float m[kMaxRows];
-  float wf[8][kMaxRows];           // per-wave rescale factors 2^(m_wave - M)
-  int last;                        // this workgroup merges the unit's splits
-  // cross-split merge (last workgroup only)
-  float2 ml[kMaxSplit * kMaxRows];  // (max, sum) per (split, row)
-  float sw[kMaxRows][kMaxSplit];    // 2^(m_split - M) per (row, split)
-  float sl[kMaxRows];               // merged denominators
-  float4 part[512];                 // per-thread partial sums of 4 dims
+  float4 part_o[512];  // cross-split merge: per-thread group partials (4 dims)
+  float2 part_ml[512]; //   and their (max, sum)
+  int last;            // this workgroup merges the unit's splits
 };
 
 // Partials cross between workgroups that may sit on different XCDs (each with
@@ -230,24 +224,27 @@ constexpr int kSc1 = 16;  // cache-policy bits of a buffer access: SC1 (device s
 // element 0 whatever the element named.)
 __device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 
+// max without NaN canonicalisation (v_maximum3_f32 on gfx950); the operands
+// here are scores, never NaN.
+__device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Cross-split merge, run by the last workgroup of a unit to finish: out =
-// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. The unit's
-// partial rows o[split][row][D] are read as 16-byte pieces spread over every
-// thread — thread t owns dims 4 (t % (D/4)) .. +4 of row (t / (D/4)) % ROWS of
-// the splits congruent to t / (ROWS*D/4) — issued together with the (max, sum)
-// pairs before any is used. One wave per row turns the pairs into per-split
-// factors (lane = split), threads fold their splits, and the groups of
-// threads sharing a (row, 4 dims) are summed through LDS. A row no split saw a
-// key for (all l_s = 0) yields zeros.
+// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. Thread t
+// owns the 4 dims 4 (t % (D/4)) .. +4 of row (t / (D/4)) % ROWS for the
+// splits congruent to t / (ROWS*D/4) modulo P: it issues all of its partial
+// loads (16-byte output pieces and (max, sum) pairs) for a batch of 8 splits
+// at once and folds them with a running max. The P groups of threads sharing
+// a (row, 4 dims) are then combined through LDS. A row no split saw a key for
+// (all l_s = 0) yields zeros.
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc, int kvh, int b,
                                              MergeLds& mg) {
   constexpr int NT = 64 * NW;
   constexpr int Q = ROWS * D / 4;  // 16-byte pieces per split
-  static_assert(Q <= NT && NT % Q == 0, "merge mapping");
+  static_assert(Q <= NT && NT % Q == 0 && NT <= 512, "merge mapping");
   constexpr int P = NT / Q;         // thread groups per piece
   constexpr int BATCH = 8;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int ns = a.n_split;
   const int piece = tid % Q, grp = tid / Q;
   const int r = piece / (D / 4), d4 = piece % (D / 4);
@@ -256,106 +253,106 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
       buffer_rsrc(a.ws_o + slot0 * D, (uint32_t)((int64_t)ns * ROWS * D * 4));
   const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.ws_ml + slot0 * 2, (uint32_t)(ns * ROWS * 8));
   const int nj = (ns - grp + P - 1) / P;  // splits grp, grp + P, ... < ns
-  // issue the first BATCH pieces and the pairs before using anything
-  u32x4_t ov[BATCH];
-#pragma unroll
-  for (int j = 0; j < BATCH; ++j) {
-    const uint32_t sp = (uint32_t)(grp + P * j);
-    ov[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                            ro, (sp * Q + piece) * 16u, 0, kSc1));  // past ns: zeros
-  }
-  for (int i = tid; i < ns * ROWS; i += NT) {
-    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rm, 8u * i, 0, kSc1));
-    mg.ml[i] = make_float2(u32_as_f32(v.x), u32_as_f32(v.y));
-  }
-  __syncthreads();
-  for (int rr = wave; rr < ROWS; rr += NW) {
-    const bool on = lane < ns;
-    const float2 ml = on ? mg.ml[lane * ROWS + rr] : make_float2(kNeg, 0.0f);
-    const float M = wave_max(ml.x);
-    const float w = on ? __builtin_amdgcn_exp2f(ml.x - M) : 0.0f;
-    const float Ls = wave_sum(ml.y * w);
-    if (on) mg.sw[rr][lane] = w;
-    if (lane == 0) mg.sl[rr] = Ls;
-  }
-  __syncthreads();
-  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float Mr = kNeg, Lr = 0.0f;
+  float4 Or = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int j0 = 0; j0 < nj; j0 += BATCH) {
-    if (j0 > 0) {
+    u32x4_t ov[BATCH];
+    uint2 mv[BATCH];
 #pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const uint32_t sp = (uint32_t)(grp + P * (j0 + j));
-        ov[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                ro, (sp * Q + piece) * 16u, 0, kSc1));
-      }
+    for (int j = 0; j < BATCH; ++j) {
+      const uint32_t sp = (uint32_t)(grp + P * (j0 + j));  // past ns: zeros, masked below
+      ov[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              ro, (sp * Q + piece) * 16u, 0, kSc1));
+      mv[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                            rm, (sp * ROWS + r) * 8u, 0, kSc1));
     }
+    float mb = Mr;
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j)
+      if (j0 + j < nj) mb = fmax_nc(mb, u32_as_f32(mv[j].x));
+    const float al = __builtin_amdgcn_exp2f(Mr - mb);
+    Lr *= al;
+    Or.x *= al; Or.y *= al; Or.z *= al; Or.w *= al;
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
       if (j0 + j < nj) {
-        const float w = mg.sw[r][grp + P * (j0 + j)];
-        acc.x = fmaf(u32_as_f32(ov[j].x), w, acc.x);
-        acc.y = fmaf(u32_as_f32(ov[j].y), w, acc.y);
-        acc.z = fmaf(u32_as_f32(ov[j].z), w, acc.z);
-        acc.w = fmaf(u32_as_f32(ov[j].w), w, acc.w);
+        const float f = __builtin_amdgcn_exp2f(u32_as_f32(mv[j].x) - mb);
+        Lr = fmaf(u32_as_f32(mv[j].y), f, Lr);
+        Or.x = fmaf(u32_as_f32(ov[j].x), f, Or.x);
+        Or.y = fmaf(u32_as_f32(ov[j].y), f, Or.y);
+        Or.z = fmaf(u32_as_f32(ov[j].z), f, Or.z);
+        Or.w = fmaf(u32_as_f32(ov[j].w), f, Or.w);
       }
     }
+    Mr = mb;
   }
-  mg.part[tid] = acc;
-  __syncthreads();
-  if (tid < Q) {
-    float4 s = mg.part[tid];
+  if constexpr (P > 1) {
+    mg.part_o[tid] = Or;
+    mg.part_ml[tid] = make_float2(Mr, Lr);
+    __syncthreads();
+    if (tid >= Q) return;
+    float M = Mr;
+#pragma unroll
+    for (int g = 1; g < P; ++g) M = fmax_nc(M, mg.part_ml[tid + g * Q].x);
+    const float f0 = __builtin_amdgcn_exp2f(Mr - M);
+    Lr *= f0;
+    Or.x *= f0; Or.y *= f0; Or.z *= f0; Or.w *= f0;
 #pragma unroll
     for (int g = 1; g < P; ++g) {
-      const float4 o = mg.part[tid + g * Q];
-      s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
+      const float2 ml = mg.part_ml[tid + g * Q];
+      const float4 o = mg.part_o[tid + g * Q];
+      const float f = __builtin_amdgcn_exp2f(ml.x - M);
+      Lr = fmaf(ml.y, f, Lr);
+      Or.x = fmaf(o.x, f, Or.x); Or.y = fmaf(o.y, f, Or.y);
+      Or.z = fmaf(o.z, f, Or.z); Or.w = fmaf(o.w, f, Or.w);
     }
-    const int rho = rc * ROWS + r;
-    const float Ls = mg.sl[r];
-    if (rho < a.rows_total) {
-      const float o4[4] = {s.x, s.y, s.z, s.w};
+  }
+  const int rho = rc * ROWS + r;
+  if (rho < a.rows_total) {
+    const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
+    const float o4[4] = {Or.x, Or.y, Or.z, Or.w};
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        store_from_f32(a.out, out_index(a, b, kvh, rho, 4 * d4 + k), OUT_DT, Ls > 0.0f ? o4[k] / Ls : 0.0f);
-    }
+    for (int k = 0; k < 4; ++k)
+      store_from_f32(a.out, out_index(a, b, kvh, rho, 4 * d4 + k), OUT_DT, o4[k] * inv);
   }
 }
 
-// Merge the partials of the NW waves — NW * PPW partial slots in o_lds, slot p
-// belonging to wave p / PPW, with (max, sum) per wave in ml_lds; the caller
-// has already passed a barrier — and store either the output (single split) or
-// this split's partial (max, sum, o). With several splits the partial is then
-// published: every wave waits until its device-scope partial stores are
-// complete, and after a barrier one thread bumps the unit's arrival counter
-// (a system-scope atomic, performed at the memory side). The workgroup that
-// arrives last merges all partials and re-arms the counter for the next call.
-template <int ROWS, int D, int OUT_DT, int NW, int PPW>
+// Workgroup epilogue. Each of the NW waves has left its partial (max, sum)
+// per row in ml_lds[w][r] and its partial output rows in o_lds[w][r][:], both
+// relative to its own max, and the caller has passed a barrier. Thread (r, d)
+// folds the NW partials of its element (every thread reads the row's NW
+// (max, sum) pairs itself, so no serial step or extra barrier is needed) and
+// either stores the output (single split) or publishes this split's partial
+// (max, sum, o). With several splits every wave then waits until its
+// device-scope partial stores are complete, and after a barrier one thread
+// bumps the unit's arrival counter (a system-scope atomic, performed at the
+// memory side). The workgroup that arrives last merges all partials and
+// re-arms the counter for the next call.
+template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int split, int rc,
                                              int kvh, int b, const float (*o_lds)[ROWS][D],
                                              const float (*ml_lds)[ROWS][2], MergeLds& mg) {
-  constexpr int NP = NW * PPW;
+  constexpr int NT = 64 * NW;
   const int tid = threadIdx.x;
   const bool single = a.n_split == 1;
-  if (tid < ROWS) {
+  for (int idx = tid; idx < ROWS * D; idx += NT) {
+    const int r = idx / D, d = idx % D;
+    float mw[NW], lw[NW];
     float M = kNeg;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_lds[w][tid][0]);
-    float Ls = 0.0f;
+    for (int w = 0; w < NW; ++w) {
+      const float2 ml = *(const float2*)&ml_lds[w][r][0];
+      mw[w] = ml.x;
+      lw[w] = ml.y;
+      M = fmax_nc(M, ml.x);
+    }
+    float Ls = 0.0f, Os = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float f = __builtin_amdgcn_exp2f(ml_lds[w][tid][0] - M);
-      mg.wf[w][tid] = f;
-      Ls += ml_lds[w][tid][1] * f;
+      const float f = __builtin_amdgcn_exp2f(mw[w] - M);
+      Ls = fmaf(lw[w], f, Ls);
+      Os = fmaf(o_lds[w][r][d], f, Os);
     }
-    mg.l[tid] = Ls;
-    mg.m[tid] = M;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < ROWS * D; idx += 64 * NW) {
-    const int r = idx / D, d = idx % D;
-    float Os = 0.0f;
-#pragma unroll
-    for (int p = 0; p < NP; ++p) Os = fmaf(o_lds[p][r][d], mg.wf[p / PPW][r], Os);
-    const float Ls = mg.l[r];
     const int rho = rc * ROWS + r;
     if (single) {
       if (rho < a.rows_total)
@@ -364,7 +361,7 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
       const int64_t slot = ((int64_t)unit * a.n_split + split) * ROWS + r;
       __hip_atomic_store(a.ws_o + slot * D + d, Os, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == 0) {
-        __hip_atomic_store(a.ws_ml + slot * 2 + 0, mg.m[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ws_ml + slot * 2 + 0, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(a.ws_ml + slot * 2 + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -392,49 +389,112 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
 // hi = (w >> 4) & 0x0F0F0F0F (elements 1,3,5,7), perm(MAGIC, lo, sel) builds
 // {0x43 | lo.byte_i, 0x43 | lo.byte_j} pairs = bf16(128 + n) (fp16: 0x64 ->
 // 1024 + n). Key dword k therefore feeds the MFMA k-order (0,2,1,3) and
-// (4,6,5,7); the staged query rows are permuted the same way.
+// (4,6,5,7); each lane's query row is held in registers permuted the same way.
 
+// Row max / row sum over a wave for the four values x[0..3] a lane holds for
+// one row set (one per query row). Two swap steps (lanes 32 apart, then rows
+// of 16 lanes) leave 16-lane row g holding row g's partial over four lanes;
+// four DPP rotations inside the 16-lane rows finish it in every lane, and
+// lane 16 g is read out. 14 VALU operations for the four rows.
+__device__ __forceinline__ float row16_max(float m) {
+  asm("s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:2 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:1 row_mask:0xf bank_mask:0xf"
+      : "+v"(m));
+  return m;
+}
+__device__ __forceinline__ float row16_sum(float m) {
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_ror:2 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_ror:1 row_mask:0xf bank_mask:0xf"
+      : "+v"(m));
+  return m;
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+template <bool SUM>
+__device__ __forceinline__ void wave_reduce4(const float x[4], float out[4]) {
+  float a0 = x[0], a2 = x[2], a1 = x[1], a3 = x[3];
+  permlane32_swap(a0, a2);  // lanes < 32: row 0 (own, lane + 32); lanes >= 32: row 2
+  permlane32_swap(a1, a3);  // lanes < 32: row 1; lanes >= 32: row 3
+  float u = SUM ? a0 + a2 : fmax_nc(a0, a2);
+  float v = SUM ? a1 + a3 : fmax_nc(a1, a3);
+  permlane16_swap(u, v);    // 16-lane row g now holds two partials of row g
+  float w = SUM ? u + v : fmax_nc(u, v);
+  w = SUM ? row16_sum(w) : row16_max(w);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[r] = readlane_f(w, 16 * r);
+}
+
+// fp32 values of the key or value scales of this lane's token for each
+// 32-dim chunk, times `mul`. raw = the token's scale row (2, 4 or 8 bytes);
+// with one scale per chunk (G = 32) chunk c is 16-bit word c, otherwise the
+// word at bit offset gsh[c].
+template <int LPT, bool S_F16>
+__device__ __forceinline__ void chunk_scales(uint2 raw, bool g32, const uint32_t (&gsh)[LPT],
+                                             float mul, float (&out)[LPT]) {
+  if (g32) {
+#pragma unroll
+    for (int c = 0; c < LPT; ++c) {
+      const uint32_t dw = c < 2 ? raw.x : raw.y;
+      float f;
+      if constexpr (S_F16) f = f16_bits_to_f32((c & 1) ? (dw >> 16) : (dw & 0xffffu));
+      else f = __builtin_bit_cast(float, (c & 1) ? (dw & 0xffff0000u) : (dw << 16));
+      out[c] = f * mul;
+    }
+  } else {
+    const uint64_t w64 = ((uint64_t)raw.y << 32) | raw.x;
+#pragma unroll
+    for (int c = 0; c < LPT; ++c)
+      out[c] = scale16_to_f32((uint32_t)(w64 >> gsh[c]) & 0xffffu, S_F16) * mul;
+  }
+}
 
 template <int D, int RS, int QM, int SM, bool ROWMASK, int NW, int CH>
 __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArgs a) {
   constexpr bool F16 = QM == KVQ_F16;
   constexpr bool S_F16 = SM == KVQ_F16;
   constexpr int LPT = D / 32;       // 32-dim chunks (16 code bytes) per token
-  constexpr int VROW = D / 2;       // code bytes per token row
-  constexpr int VLD = VROW * 64 / 1024;  // 16-byte V loads per lane per 64-token tile
+  constexpr int KD = D / 8;         // code dwords per token row
   constexpr int VLPT = D / 8;       // PV lanes per token row (one code dword each)
   constexpr int VTS = 64 / VLPT;    // PV token subsets
   constexpr int SUB = 4 * VTS;      // tokens per PV sub-tile
   constexpr int NSUB = 64 / SUB;    // PV sub-tiles per 64-token tile
   constexpr int ROWS = 4 * RS;
-  constexpr int QT = ROWS * D / 8;  // threads staging the query rows, 8 elements each
   constexpr uint32_t MAGIC = F16 ? 0x64646464u : 0x43434343u;
   constexpr uint32_t NEG_BIAS = F16 ? 0xE408E408u : 0xC308C308u;  // {-1032, -1032} / {-136, -136}
   constexpr uint32_t SEL_02 = 0x04010400u;  // {MAGIC | byte0, MAGIC | byte1}
   constexpr uint32_t SEL_46 = 0x04030402u;  // {MAGIC | byte2, MAGIC | byte3}
-  static_assert(QT <= 64 * NW, "query staging");
 
-  // Per wave: the V codes of the tile being consumed (row-major image of the
-  // tile, 64 x VROW bytes) and its softmax weights, [rowset][subtile] blocks of
+  // Per wave: the softmax weights of the tile, [rowset][subtile] blocks of
   // 4 * LPT * VTS * 4 bf16 in which (row, chunk) pair rc = 4 * chunk + row,
   // token subset ts and position k sit at ((rc ^ subtile) * VTS + ts) * 4 + k:
   // a PV read (one subtile, every (rc, ts)) covers one contiguous block and a
   // token-lane write (one rc, every token) spreads its subtiles over distinct
   // banks. Once the sequence loop is done the same bytes hold the per-wave
   // partial outputs.
-  constexpr int V_BYTES = NW * 64 * VROW;
   constexpr int W_BYTES = NW * RS * 4 * LPT * NSUB * VTS * 4 * 2;
   constexpr int O_BYTES = NW * ROWS * D * 4;
-  constexpr int S_BYTES = V_BYTES + W_BYTES > O_BYTES ? V_BYTES + W_BYTES : O_BYTES;
+  constexpr int S_BYTES = W_BYTES > O_BYTES ? W_BYTES : O_BYTES;
   // query rows padded by 16 bytes so the four rows a QK read touches sit in
   // different LDS banks
   constexpr int QROW = D / 2 + 4;
-  __shared__ __attribute__((aligned(16))) uint32_t q_lds[ROWS][QROW];
+  __shared__ __attribute__((aligned(16))) uint32_t q_lds[NW][ROWS][QROW];
   __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
-  __shared__ float ml_lds[NW][ROWS][2];
+  __shared__ __attribute__((aligned(16))) float ml_lds[NW][ROWS][2];
   __shared__ MergeLds mg;
-  auto v_lds = reinterpret_cast<uint8_t(*)[64 * VROW]>(smem);
-  auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem + V_BYTES);
+  auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem);
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
   const int tid = threadIdx.x;
@@ -470,6 +530,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vp_bh, Le * vps);
   const __amdgpu_buffer_rsrc_t rvs = buffer_rsrc(vs_bh, Le * vss2);
   const int ng = (D + a.G - 1) / a.G;  // scales per token row: 1, 2 or 4 (wave-uniform)
+  const bool g32 = a.G == 32;
   uint32_t gsh[LPT];  // bit offset of each 32-dim chunk's scale in the loaded scale row
 #pragma unroll
   for (int c = 0; c < LPT; ++c) gsh[c] = 16u * (uint32_t)((c * 32) / a.G);
@@ -482,24 +543,16 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const int w_sub = lane / SUB;             // sub-tile of token `lane`
   const int w_ts = (lane % SUB) % VTS;      // its token subset
   const int w_k = (lane % SUB) / VTS;       // its position in the subset
-  // V loads: load j of a lane covers bytes [1024 j + 16 lane, +16) of the
-  // tile's row-major image: token (1024 j + 16 lane) / VROW of the tile.
-  uint32_t v_tok[VLD], v_off[VLD];
-#pragma unroll
-  for (int j = 0; j < VLD; ++j) {
-    v_tok[j] = (uint32_t)((1024 * j + 16 * lane) / VROW);
-    v_off[j] = (uint32_t)((1024 * j + 16 * lane) % VROW);
-  }
 
   // Register slots for CH tiles of 64 tokens. Tile i of a chunk is computed
   // start to finish before tile i + 1, and each of its parts is refilled for
   // the next chunk as soon as it is consumed, so loads overlap the math.
   // Per tile and lane: the lane's token's K row (LPT x 16 bytes), its K and V
-  // scale rows (one 2/4/8-byte load each) and VLD 16-byte pieces of the V
-  // tile — 6 to 10 wide loads per tile and wave.
+  // scale rows (one 2/4/8-byte load each) and, in the PV layout, code dword
+  // vj of the 4 * NSUB tokens (s * SUB + VTS * k + vts) it multiplies.
   u32x4_t kc4[CH][LPT];
   uint2 skr[CH], svr[CH];
-  u32x4_t vq[CH][VLD];
+  uint32_t vq[CH][NSUB][4];
   auto load_scales = [&](__amdgpu_buffer_rsrc_t r, uint32_t off) -> uint2 {
     if (ng >= 4) return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
     if (ng == 2) return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0), 0u);
@@ -517,88 +570,98 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     const uint32_t t0 = tile_t0(i, base);
     svr[i] = load_scales(rvs, (t0 + lane) * vss2);
 #pragma unroll
-    for (int j = 0; j < VLD; ++j)
-      vq[i][j] = __builtin_bit_cast(u32x4_t,
-                                    __builtin_amdgcn_raw_buffer_load_b128(rv, (t0 + v_tok[j]) * vps + v_off[j], 0, 0));
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        vq[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(
+            rv, (t0 + (uint32_t)(s * SUB + VTS * k + vts)) * vps + 4u * (uint32_t)vj, 0, 0);
   };
-  // ---- query loads go out first (threads < QT; thread (q_r, q_k) reads
-  //      elements [8 q_k, 8 q_k + 8) of row q_r; rows past the last one read
-  //      row 0 and are zeroed) ----
-  const int q_r = tid / (D / 8), q_k = tid % (D / 8);
-  const bool q_ok = rc * ROWS + q_r < a.rows_total;
-  uint4 qraw = make_uint4(0u, 0u, 0u, 0u);  // elements (e0,e1) (e2,e3) (e4,e5) (e6,e7)
-  if (tid < QT) {
-    const int rho = q_ok ? rc * ROWS + q_r : 0;
-    const int head = kvh * a.ratio + rho / a.Sq, qi = rho % a.Sq;
+
+  // ---- loads: the query rows first (wave-private copy: QT pieces of 8
+  //      elements, lane handles pieces lane, lane + 64, ...; rows past the last
+  //      one read row 0 and are zeroed), then the first tiles' cache rows, so
+  //      the query is waited for without waiting for the cache. Tile 0's
+  //      loads are unconditional (a wave without a tile reads past the split's
+  //      end: zeros, no memory traffic). ----
+  constexpr int QT = ROWS * D / 8;
+  constexpr int QPL = (QT + 63) / 64;  // query pieces per lane
+  uint4 qraw[QPL];
+#pragma unroll
+  for (int j = 0; j < QPL; ++j) {
+    const int g = lane + 64 * j;
+    const int q_r = (g / (D / 8)) % ROWS, q_k = g % (D / 8);
+    const int rho = rc * ROWS + q_r;
+    const int rho_c = rho < a.rows_total ? rho : 0;
+    const int head = kvh * a.ratio + rho_c / a.Sq, qi = rho_c % a.Sq;
     const int64_t qoff = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
                          (int64_t)(8 * q_k) * a.qs_d;
+    const uint16_t* q16 = (const uint16_t*)a.q + qoff;
     if (a.q_vec) {
-      qraw = *(const uint4*)((const uint16_t*)a.q + qoff);  // used only after the cache loads
+      qraw[j] = *(const uint4*)q16;
     } else {
-      const uint16_t* q16 = (const uint16_t*)a.q + qoff;
       uint32_t e[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) e[j] = q16[(int64_t)j * a.qs_d];
-      qraw = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+      for (int k = 0; k < 8; ++k) e[k] = q16[(int64_t)k * a.qs_d];
+      qraw[j] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
     }
   }
-
-  // With one row set the first chunk's loads go out before the query is
-  // staged; two row sets load each chunk at the top of the loop. Tile 0's
-  // loads are unconditional (a wave without a tile reads past the split's
-  // end: zeros, no memory traffic), which keeps the compiler's wait for the
-  // query exact.
-  constexpr bool PIPE = RS == 1;
-  if constexpr (PIPE) {
-    load_k(0, wave);
-    load_v(0, wave);
-#pragma unroll
-    for (int i = 1; i < CH; ++i) {
-      if (wave + NW * i < ntiles) {
-        load_k(i, wave);
-        load_v(i, wave);
-      }
-    }
-  }
-
-  // ---- query rows -> LDS, permuted to the key operand order ----
-  if (tid < QT) {
-    const uint32_t keep = q_ok ? 0xffffffffu : 0u;
-    const uint32_t x = qraw.x & keep, y = qraw.y & keep, z = qraw.z & keep, w = qraw.w & keep;
-    const u32x4_t qp = {__builtin_amdgcn_perm(y, x, 0x05040100u), __builtin_amdgcn_perm(y, x, 0x07060302u),
-                        __builtin_amdgcn_perm(w, z, 0x05040100u), __builtin_amdgcn_perm(w, z, 0x07060302u)};
-    *(u32x4_t*)&q_lds[q_r][4 * q_k] = qp;  // (e0,e2) (e1,e3) (e4,e6) (e5,e7)
-  }
-  __syncthreads();
-
-  // ---- this lane's query row (row lane % 4 of each row set) and the
-  //      accumulator init -bias * sum(q) per 32-dim chunk, on the MFMA ----
-  const int my_row = lane & 3;
-  f32x4_t qinit[RS][LPT];
   int lim[RS][4];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rho = rc * ROWS + rs * 4 + i;
-      int lm = a.causal ? L - a.Sq + (rho % a.Sq) + 1 : L;
+      const int rr = rc * ROWS + rs * 4 + i;
+      int lm = a.causal ? L - a.Sq + (rr % a.Sq) + 1 : L;
       lm = lm < 0 ? 0 : lm;
-      lim[rs][i] = rho < a.rows_total ? lm : 0;
+      lim[rs][i] = rr < a.rows_total ? lm : 0;
     }
+  }
+  load_k(0, wave);
+  load_v(0, wave);
+#pragma unroll
+  for (int i = 1; i < CH; ++i) {
+    if (wave + NW * i < ntiles) {
+      load_k(i, wave);
+      load_v(i, wave);
+    }
+  }
+  // query rows -> this wave's LDS copy, permuted to the key operand order:
+  // (e0,e2) (e1,e3) (e4,e6) (e5,e7) of every 8 elements
+#pragma unroll
+  for (int j = 0; j < QPL; ++j) {
+    const int g = lane + 64 * j;
+    if (g < QT) {
+      const int q_r = g / (D / 8), q_k = g % (D / 8);
+      const uint32_t keep = rc * ROWS + q_r < a.rows_total ? 0xffffffffu : 0u;
+      const uint4 raw = qraw[j];
+      const uint32_t x = raw.x & keep, y = raw.y & keep, z = raw.z & keep, w = raw.w & keep;
+      *(u32x4_t*)&q_lds[wave][q_r][4 * q_k] =
+          u32x4_t{__builtin_amdgcn_perm(y, x, 0x05040100u), __builtin_amdgcn_perm(y, x, 0x07060302u),
+                  __builtin_amdgcn_perm(w, z, 0x05040100u), __builtin_amdgcn_perm(w, z, 0x07060302u)};
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int my_row = lane & 3;
+  // accumulator init -bias * sum(q) per 32-dim chunk, on the MFMA
+  f32x4_t qinit[RS][LPT];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
     for (int c = 0; c < LPT; ++c) {
       f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) {
-        const u32x4_t qv = *(const u32x4_t*)&q_lds[rs * 4 + my_row][16 * c + 4 * k4];
-        acc = mfma4<F16>(qv.x, qv.y, NEG_BIAS, NEG_BIAS, acc);
-        acc = mfma4<F16>(qv.z, qv.w, NEG_BIAS, NEG_BIAS, acc);
+        const u32x4_t q4 = *(const u32x4_t*)&q_lds[wave][rs * 4 + my_row][16 * c + 4 * k4];
+        acc = mfma4<F16>(q4.x, q4.y, NEG_BIAS, NEG_BIAS, acc);
+        acc = mfma4<F16>(q4.z, q4.w, NEG_BIAS, NEG_BIAS, acc);
       }
       qinit[rs][c] = acc;
     }
   }
 
-  // ---- running softmax state ----
+  // ---- running softmax state (base 2; scores carry sm_scale * log2 e) ----
   float m_run[RS][4], l_acc[RS][4];
   f32x4_t o_acc[RS][8], w_acc[RS];
 #pragma unroll
@@ -613,21 +676,14 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     w_acc[rs] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  uint8_t* my_v = v_lds[wave];
+  bool fresh = true;  // no tile folded into the running state yet (wave-uniform)
   for (int base = wave; base < ntiles; base += NW * CH) {
-    if constexpr (!PIPE) {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        if (base + NW * i < ntiles) {
-          load_k(i, base);
-          load_v(i, base);
-        }
-      }
-    }
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       if (base + NW * i >= ntiles) break;  // wave-uniform: this wave has no tile i
-      const bool refill = PIPE && base + NW * (CH + i) < ntiles;
+      const bool refill = base + NW * (CH + i) < ntiles;
+      const int t0 = t_begin + (base + NW * i) * 64;
+      const bool masked = ROWMASK || t0 + 64 > t_end;  // wave-uniform
       // ---- QK on the matrix cores: scores of token `lane` for every row ----
       float sc[RS][4];
       {
@@ -649,86 +705,97 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
             const uint32_t b57 = __builtin_amdgcn_perm(MAGIC, hi, SEL_46);  // (e5, e7)
 #pragma unroll
             for (int rs = 0; rs < RS; ++rs) {
-              const u32x4_t qv = *(const u32x4_t*)&q_lds[rs * 4 + my_row][4 * kd];
-              acc[rs][c] = mfma4<F16>(qv.x, qv.y, b02, b13, acc[rs][c]);
-              acc[rs][c] = mfma4<F16>(qv.z, qv.w, b46, b57, acc[rs][c]);
+              const u32x4_t q4 = *(const u32x4_t*)&q_lds[wave][rs * 4 + my_row][4 * kd];
+              acc[rs][c] = mfma4<F16>(q4.x, q4.y, b02, b13, acc[rs][c]);
+              acc[rs][c] = mfma4<F16>(q4.z, q4.w, b46, b57, acc[rs][c]);
             }
           }
         }
-        const int t = t_begin + (base + NW * i) * 64 + lane;
-        const bool tok_ok = t < t_end;
-        const uint64_t skw = ((uint64_t)skr[i].y << 32) | skr[i].x;
         float skl[LPT];
-#pragma unroll
-        for (int c = 0; c < LPT; ++c)
-          skl[c] = scale16_to_f32((uint32_t)(skw >> gsh[c]) & 0xffffu, S_F16) * a.scale_log2;
+        chunk_scales<LPT, S_F16>(skr[i], g32, gsh, a.scale_log2, skl);
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float s = 0.0f;
+            float s = acc[rs][0][r] * skl[0];
 #pragma unroll
-            for (int c = 0; c < LPT; ++c) s = fmaf(acc[rs][c][r], skl[c], s);
-            bool ok = tok_ok;
-            if constexpr (ROWMASK) ok = ok && (t < lim[rs][r]);
-            sc[rs][r] = ok ? s : kNeg;
+            for (int c = 1; c < LPT; ++c) s = fmaf(acc[rs][c][r], skl[c], s);
+            sc[rs][r] = s;
           }
+        }
+        if (masked) {
+          const int t = t0 + lane;
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              bool ok = t < t_end;
+              if constexpr (ROWMASK) ok = ok && (t < lim[rs][r]);
+              sc[rs][r] = ok ? sc[rs][r] : kNeg;
+            }
         }
       }
       if (refill) load_k(i, base + NW * CH);
 
-      // ---- V codes of this tile -> the wave's LDS image ----
+      // ---- tile max, rescale of the running state (not for a wave's
+      //      first tile: its accumulators are still zero) ----
+      {
+        float mt[RS][4];
 #pragma unroll
-      for (int j = 0; j < VLD; ++j) *(u32x4_t*)&my_v[1024 * j + 16 * lane] = vq[i][j];
-
-      // ---- tile max and rescale of the running state ----
-      bool grow = false;
-      float m_new[RS][4];
+        for (int rs = 0; rs < RS; ++rs) wave_reduce4<false>(sc[rs], mt[rs]);
+        if (fresh) {
 #pragma unroll
-      for (int rs = 0; rs < RS; ++rs) {
+          for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          m_new[rs][r] = fmaxf(m_run[rs][r], wave_max(sc[rs][r]));
-          grow = grow || (m_new[rs][r] > m_run[rs][r]);
-        }
-      }
-      if (grow) {
+            for (int r = 0; r < 4; ++r) m_run[rs][r] = mt[rs][r];
+        } else {
+          bool grow = false;
 #pragma unroll
-        for (int rs = 0; rs < RS; ++rs) {
-          f32x4_t al;
+          for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            al[r] = __builtin_amdgcn_exp2f(m_run[rs][r] - m_new[rs][r]);
-            l_acc[rs][r] *= al[r];
-            m_run[rs][r] = m_new[rs][r];
+            for (int r = 0; r < 4; ++r) grow = grow || (mt[rs][r] > m_run[rs][r]);
+          if (grow) {
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) {
+              f32x4_t al;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float mn = fmax_nc(m_run[rs][r], mt[rs][r]);
+                al[r] = __builtin_amdgcn_exp2f(m_run[rs][r] - mn);
+                l_acc[rs][r] *= al[r];
+                m_run[rs][r] = mn;
+              }
+#pragma unroll
+              for (int m = 0; m < 8; ++m) o_acc[rs][m] *= al;
+              w_acc[rs] *= al;
+            }
           }
-#pragma unroll
-          for (int m = 0; m < 8; ++m) o_acc[rs][m] *= al;
-          w_acc[rs] *= al;
         }
+        fresh = false;
       }
 
       // ---- p and w = p * v_scale (bf16) -> LDS ----
       {
-        const uint64_t svw = ((uint64_t)svr[i].y << 32) | svr[i].x;
         float svl[LPT];
-#pragma unroll
-        for (int c = 0; c < LPT; ++c) svl[c] = scale16_to_f32((uint32_t)(svw >> gsh[c]) & 0xffffu, S_F16);
+        chunk_scales<LPT, S_F16>(svr[i], g32, gsh, 1.0f, svl);
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float s = sc[rs][r];
-            const float p = s > kNeg ? __builtin_amdgcn_exp2f(s - m_run[rs][r]) : 0.0f;
+            float p = __builtin_amdgcn_exp2f(s - m_run[rs][r]);
+            if (masked) p = s > kNeg ? p : 0.0f;
             l_acc[rs][r] += p;
 #pragma unroll
-            for (int c = 0; c < LPT; ++c)
-              w_lds[wave][rs][w_sub][(((4 * c + r) ^ w_sub) * VTS + w_ts) * 4 + w_k] =
-                  __builtin_bit_cast(uint16_t, (__bf16)(p * svl[c]));
+            for (int c = 0; c < LPT; c += 2) {
+              const bf16x2_t pk2 = {(__bf16)(p * svl[c]), (__bf16)(p * svl[c + 1])};
+              const uint32_t pk = __builtin_bit_cast(uint32_t, pk2);
+              w_lds[wave][rs][w_sub][(((4 * c + r) ^ w_sub) * VTS + w_ts) * 4 + w_k] = (uint16_t)pk;
+              w_lds[wave][rs][w_sub][(((4 * c + 4 + r) ^ w_sub) * VTS + w_ts) * 4 + w_k] = (uint16_t)(pk >> 16);
+            }
           }
         }
       }
-      if (refill) load_v(i, base + NW * CH);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -738,14 +805,10 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       // and high nibbles then give (token0, token1) pairs of one dim per perm.
 #pragma unroll
       for (int s = 0; s < NSUB; ++s) {
-        uint32_t vc[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          vc[k] = *(const uint32_t*)&my_v[(s * SUB + VTS * k + vts) * VROW + 4 * vj];
         uint32_t bp[2][8];  // [token pair][dim within the lane's 8]
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
-          const uint32_t v0 = vc[2 * tp], v1 = vc[2 * tp + 1];
+          const uint32_t v0 = vq[i][s][2 * tp], v1 = vq[i][s][2 * tp + 1];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {  // dims 0-3, dims 4-7
             const uint32_t u = __builtin_amdgcn_perm(v1, v0, hh ? 0x07030602u : 0x05010400u);
@@ -765,6 +828,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
           w_acc[rs] = mfma4<false>(wa.x, wa.y, kBf16OnePair, kBf16OnePair, w_acc[rs]);
         }
       }
+      if (refill) load_v(i, base + NW * CH);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -778,7 +842,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   //      (permlane16 swap) or 8 (row rotate, D = 64) apart, and each lane keeps
   //      the half its side of the pair owns. Afterwards the lane of subset g
   //      holds values [g * N / VTS, (g + 1) * N / VTS). Then -> LDS (over the
-  //      V/weight bytes, so every wave must be done with those). ----
+  //      weight bytes, so every wave must be done with those). ----
   constexpr int NV = 32 * RS;
   float val[NV];
 #pragma unroll
@@ -810,25 +874,9 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     }
   }
   constexpr int NK = NV / VTS;  // values a lane keeps
-  // row sums of the softmax denominators: rows 0-3 of each row set land in
-  // lane groups 0-3 after the two swaps, then a 16-lane row reduction
   float lsum[RS][4];
 #pragma unroll
-  for (int rs = 0; rs < RS; ++rs) {
-    float l0 = l_acc[rs][0], l2 = l_acc[rs][2], l1 = l_acc[rs][1], l3 = l_acc[rs][3];
-    permlane32_swap(l0, l2);
-    permlane32_swap(l1, l3);
-    float x = l0 + l2, y = l1 + l3;
-    permlane16_swap(x, y);
-    float v = x + y;
-    v += dpp<0x111>(v, 0.0f);  // row_shr:1
-    v += dpp<0x112>(v, 0.0f);  // row_shr:2
-    v += dpp<0x114>(v, 0.0f);  // row_shr:4
-    v += dpp<0x118>(v, 0.0f);  // row_shr:8 -> lane 15 of each row holds the row's total
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      lsum[rs][r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r + 15));
-  }
+  for (int rs = 0; rs < RS; ++rs) wave_reduce4<true>(l_acc[rs], lsum[rs]);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < NK; i += 4) {
@@ -846,7 +894,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     }
   }
   __syncthreads();
-  finish_block<ROWS, D, QM, NW, 1>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
+  finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
 }
 
 // ===========================================================================
@@ -867,7 +915,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
 
   __shared__ __attribute__((aligned(16))) WT w_lds[4][CH][ROWS][LPT][TPT];
   __shared__ float o_lds[4][ROWS][D];
-  __shared__ float ml_lds[4][ROWS][2];
+  __shared__ __attribute__((aligned(16))) float ml_lds[4][ROWS][2];
   __shared__ MergeLds mg;
 
   const int tid = threadIdx.x;
@@ -1128,7 +1176,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     }
   }
   __syncthreads();
-  finish_block<ROWS, D, QM, 4, 1>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
+  finish_block<ROWS, D, QM, 4>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
 }
 
 // ---------------------------------------------------------------------------
