@@ -108,10 +108,12 @@ int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t S
                                    int64_t num_cus);
 
 /*
- * Workspace (device bytes) kvq_decode_attn needs for `n_split` splits. The
- * workspace must be zero-filled once before its first use; the kernel leaves
- * its counters at zero again on exit, so it can be reused by later calls on the
- * same stream. Calls that overlap in time must not share a workspace.
+ * Workspace (device bytes) kvq_decode_attn needs for `n_split` splits: a fixed
+ * 320 KiB block of per-(batch, KV head) arrival counters, then the splits'
+ * partial results. The workspace must be zero-filled once before its first
+ * use; the kernel leaves its counters at zero again on exit, so it can be
+ * reused by later calls on the same stream, with any plan. Calls that overlap
+ * in time must not share a workspace.
  */
 int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
                                         int64_t D, int q_dtype, int scale_dtype,

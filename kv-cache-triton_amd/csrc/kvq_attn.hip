@@ -72,6 +72,8 @@ struct AttnArgs {
 
 constexpr float kNeg = -1.0e30f;
 constexpr int kMaxSplit = 64;  // split-K fan-out cap (bounds the merge's LDS)
+constexpr int kSubCnt = 4;      // arrival sub-counters per unit
+constexpr int kCntStride = 16;  // uint32 words between counters (64 bytes)
 constexpr uint32_t kNibPairs = 0x000F000Fu;
 constexpr uint32_t kBf16Magic = 0x43004300u;  // bf16(128), bf16(128)
 constexpr uint32_t kF16Magic = 0x64006400u;   // fp16(1024), fp16(1024)
@@ -325,9 +327,15 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
 // either stores the output (single split) or publishes this split's partial
 // (max, sum, o). With several splits every wave then waits until its
 // device-scope partial stores are complete, and after a barrier one thread
-// bumps the unit's arrival counter (a system-scope atomic, performed at the
-// memory side). The workgroup that arrives last merges all partials and
-// re-arms the counter for the next call.
+// records the arrival. Arrivals are counted in two levels so that no counter
+// sees more than about eight increments per call (same-address atomics are
+// performed one after another at the memory side, and the last arrival would
+// otherwise queue behind the whole unit): split s increments sub-counter
+// s % kSubCnt of its unit; the workgroup that completes a sub-counter
+// increments the unit's top counter; the one that completes the top counter
+// arrived last, merges all partials, and re-arms the counters (each completer
+// re-arms the counter it completed) for the next call. Plans with fewer than
+// 2 * kSubCnt splits count on the top counter alone.
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int split, int rc,
                                              int kvh, int b, const float (*o_lds)[ROWS][D],
@@ -370,14 +378,31 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are complete
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(a.ws_cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    mg.last = prev == (uint32_t)(a.n_split - 1) ? 1 : 0;
+    const int ns = a.n_split;
+    uint32_t* cnt = a.ws_cnt + (int64_t)unit * kCntStride * (kSubCnt + 1);  // [top, sub 0..]
+    bool last;
+    if (ns >= 2 * kSubCnt) {
+      const int g = split % kSubCnt;
+      uint32_t* sub = cnt + (g + 1) * kCntStride;
+      const uint32_t n_g = (uint32_t)((ns - g + kSubCnt - 1) / kSubCnt);
+      last = false;
+      if (__hip_atomic_fetch_add(sub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == n_g - 1u) {
+        __hip_atomic_store(sub, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+               (uint32_t)(kSubCnt - 1);
+      }
+    } else {
+      last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+             (uint32_t)(ns - 1);
+    }
+    mg.last = last ? 1 : 0;
   }
   __syncthreads();
   if (!mg.last) return;
   merge_splits<ROWS, D, OUT_DT, NW>(a, unit, rc, kvh, b, mg);
-  if (tid == 0) __hip_atomic_store(a.ws_cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (tid == 0)
+    __hip_atomic_store(a.ws_cnt + (int64_t)unit * kCntStride * (kSubCnt + 1), 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // ===========================================================================
@@ -1227,14 +1252,18 @@ static int make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, 
   }
   ns = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ns, max_split), kMaxSplit));
   if (units * ns > 0x7fffffffll || units * p->rows * D / 128 >= 0x7fffffffll) return KVQ_EUNSUP;
+  if (ns > 1 && units > 1024) return KVQ_EUNSUP;  // split plans keep their counters in a fixed block
   p->n_split = (int)ns;
   return KVQ_OK;
 }
 
-// Workspace: the per-unit arrival counters (a 256-byte block), per (unit,
-// split, row) the partial (max, sum) pair (padded to 256 bytes), then the
-// partial output rows.
-static int64_t ws_cnt_bytes(const Plan& p) { return ((int64_t)p.n_units * 4 + 255) / 256 * 256; }
+// Workspace: a fixed block of per-unit arrival counters (one top and kSubCnt
+// sub-counters per unit, 64 bytes apart; the same bytes for every plan, so a
+// workspace reused by calls with different plans never reads another plan's
+// partials as counters), per (unit, split, row) the partial (max, sum) pair
+// (padded to 256 bytes), then the partial output rows.
+constexpr int64_t kCntUnits = 1024;  // units a split plan may have
+static int64_t ws_cnt_bytes(const Plan&) { return kCntUnits * (kSubCnt + 1) * kCntStride * 4; }
 static int64_t ws_ml_bytes(const Plan& p) {
   const int64_t slots = (int64_t)p.n_units * p.n_split * p.rows;
   return (slots * 2 * 4 + 255) / 256 * 256;

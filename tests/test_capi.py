@@ -58,8 +58,8 @@ def test_workspace_bytes():
     B16 = nat.KVQ_BF16
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 1) == 0
     ws = lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 32)
-    # 8 units x 32 splits x 4 rows x (128 + 2) floats, plus 256-byte counter and padding blocks
-    assert ws >= 8 * 32 * 4 * 130 * 4 and ws < 8 * 32 * 4 * 130 * 4 + 1024
+    # counter block (1024 units x 5 counters x 64 bytes), then 8 units x 32 splits x 4 rows x (128 + 2) floats
+    assert ws == 1024 * 5 * 64 + 8 * 32 * 4 * 130 * 4
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, 7, B16, 4) == nat.KVQ_EINVAL
 
 
