@@ -539,7 +539,19 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   }
   int t_begin, t_end;
   split_range(a, L, split, t_begin, t_end);
-  const int ntiles = t_end > t_begin ? (t_end - t_begin + 63) / 64 : 0;
+  // Tiles of 64 keys, dealt to the waves round-robin. A split of whole passes
+  // (NW tiles each) plus at most NW keys does not open another pass for those
+  // few keys (it would cost one wave a whole tile): wave w folds tail key w
+  // into its partial at the end with a short VALU dot product.
+  int ntiles = t_end > t_begin ? (t_end - t_begin + 63) / 64 : 0;
+  int n_tail = 0;
+  {
+    const int full = (t_end - t_begin) / 64, rem = (t_end - t_begin) % 64;
+    if (rem > 0 && rem <= NW && full > 0 && full % NW == 0) {
+      ntiles = full;
+      n_tail = rem;
+    }
+  }
 
   // ---- cache slices as bounds-checked buffers (rows >= L read as zero) ----
   const uint8_t* kp_bh = a.kp + (int64_t)b * a.kps_b + (int64_t)kvh * a.kps_h;
@@ -649,6 +661,18 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       load_k(i, wave);
       load_v(i, wave);
     }
+  }
+  // tail key of this wave (if any): lane l holds code byte l of its K and V
+  // rows (dims 2l, 2l+1) and the scales of their group
+  const int tail_t = t_begin + 64 * ntiles + wave;
+  uint32_t tail_kb = 0u, tail_vb = 0u, tail_ks = 0u, tail_vs = 0u;
+  if (wave < n_tail) {
+    const uint32_t tt = (uint32_t)tail_t, col = (uint32_t)(lane % (D / 2));
+    const uint32_t sg = 2u * (uint32_t)((2 * (lane % (D / 2))) / a.G);
+    tail_kb = __builtin_amdgcn_raw_buffer_load_b8(rk, tt * kps + col, 0, 0);
+    tail_vb = __builtin_amdgcn_raw_buffer_load_b8(rv, tt * vps + col, 0, 0);
+    tail_ks = __builtin_amdgcn_raw_buffer_load_b16(rks, tt * kss2 + sg, 0, 0);
+    tail_vs = __builtin_amdgcn_raw_buffer_load_b16(rvs, tt * vss2 + sg, 0, 0);
   }
   // query rows -> this wave's LDS copy, permuted to the key operand order:
   // (e0,e2) (e1,e3) (e4,e6) (e5,e7) of every 8 elements
@@ -915,6 +939,65 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       for (int r = 0; r < 4; ++r) {
         ml_lds[wave][rs * 4 + r][0] = m_run[rs][r];
         ml_lds[wave][rs * 4 + r][1] = lsum[rs][r];
+      }
+    }
+  }
+  // ---- tail key of this wave: score s_r = q_r . k (lanes own dims 2l, 2l+1,
+  //      summed over the wave), then the wave's partial absorbs it:
+  //      M = max(m, s), o = o 2^(m - M) + v 2^(s - M), l = l 2^(m - M) + 2^(s - M) ----
+  if (wave < n_tail) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool col_ok = lane < D / 2;
+    const float ksf = scale16_to_f32(tail_ks, S_F16), vsf = scale16_to_f32(tail_vs, S_F16);
+    const float k0 = col_ok ? ((float)(int)(tail_kb & 15u) - 8.0f) * ksf : 0.0f;
+    const float k1 = col_ok ? ((float)(int)((tail_kb >> 4) & 15u) - 8.0f) * ksf : 0.0f;
+    const float v0 = ((float)(int)(tail_vb & 15u) - 8.0f) * vsf;
+    const float v1 = ((float)(int)((tail_vb >> 4) & 15u) - 8.0f) * vsf;
+    // query elements 2l, 2l+1 from the permuted copy: element pairs of each 8
+    // sit as (e0,e2) (e1,e3) (e4,e6) (e5,e7)
+    const int lc = lane % (D / 2), kd = lc / 4, jj = lc % 4;
+    const int dwa = 4 * kd + 2 * (jj >> 1);
+    const bool hi = (jj & 1) != 0;
+    float st[RS][4];
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t qa = q_lds[wave][rs * 4 + r][dwa], qb = q_lds[wave][rs * 4 + r][dwa + 1];
+        const uint32_t ha = hi ? (qa >> 16) : (qa & 0xffffu), hb = hi ? (qb >> 16) : (qb & 0xffffu);
+        const float q0 = F16 ? f16_bits_to_f32(ha) : bf16_bits_to_f32(ha);
+        const float q1 = F16 ? f16_bits_to_f32(hb) : bf16_bits_to_f32(hb);
+        st[rs][r] = fmaf(q0, k0, q1 * k1);
+      }
+      float tot[4];
+      wave_reduce4<true>(st[rs], tot);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bool ok = true;
+        if constexpr (ROWMASK) ok = tail_t < lim[rs][r];
+        st[rs][r] = ok ? tot[r] * a.scale_log2 : kNeg;
+      }
+    }
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = rs * 4 + r;
+        const float m_old = ml_lds[wave][row][0], l_old = ml_lds[wave][row][1];
+        const float sv = st[rs][r];
+        const float M = fmax_nc(m_old, sv);
+        const float fa = __builtin_amdgcn_exp2f(m_old - M);
+        const float fb = sv > kNeg ? __builtin_amdgcn_exp2f(sv - M) : 0.0f;
+        if (col_ok) {
+          const float2 o2 = *(const float2*)&o_lds[wave][row][2 * lc];
+          *(float2*)&o_lds[wave][row][2 * lc] = make_float2(fmaf(o2.x, fa, v0 * fb), fmaf(o2.y, fa, v1 * fb));
+        }
+        if (lane == 0) {
+          ml_lds[wave][row][0] = M;
+          ml_lds[wave][row][1] = fmaf(l_old, fa, fb);
+        }
       }
     }
   }

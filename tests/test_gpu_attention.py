@@ -166,6 +166,25 @@ def test_repeat_calls_are_identical():
     assert np.abs(c.float().cpu().numpy() - want).max() <= 2e-2
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,dtype,causal", [
+    (1, 32, 8, 1, 16385, 128, "bf16", False),   # one split of 512 + 1 keys
+    (1, 32, 8, 1, 16640, 128, "bf16", False),   # every split 512 + 8 keys (one per wave)
+    (1, 64, 8, 1, 8288, 128, "bf16", False),    # 8 query rows, 4 waves: splits of 256 + 3
+    (1, 8, 4, 2, 32896, 128, "bf16", True),     # causal query block, splits of 512 + 2
+    (1, 16, 4, 1, 32832, 64, "f16", False),     # D = 64, splits of 512 + 1
+])
+def test_split_tail_keys(B, Hq, Hkv, Sq, Sk, D, dtype, causal):
+    """Splits of whole passes plus at most one key per wave fold those keys in
+    with the per-wave tail path instead of another tile pass."""
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, seed=Sk % 97)
+    out = attention_forward_quant_gqa(q.to(DEV), kp, ks, vp, vs, n_q_heads=Hq, n_kv_heads=Hkv,
+                                      is_causal=causal)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got - _oracle(q, kp, ks, vp, vs, 32, causal=causal)).max()
+    assert err <= 2e-2, err
+
+
 def test_validation_errors():
     # tests/llama3/test_attention_quant_gqa.py:123-141
     q, kp, ks, vp, vs = _inputs(1, 8, 4, 1, 32, 128, "bf16", seed=0)
