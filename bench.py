@@ -78,6 +78,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=0, help="override the workload's layer count")
     ap.add_argument("--ctx", type=int, default=0, help="override the workload's context length")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a HIP graph")
+    ap.add_argument("--unfused", action="store_true",
+                    help="three launches per layer (quantize K, quantize V, attention) instead of the "
+                         "fused decode step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -159,7 +162,19 @@ def main() -> int:
     # ragged: each sequence attends its own length plus the new token
     seq_plus = (seq_lens + 1) if seq_lens is not None else None
 
+    # The fused decode step (one launch per layer: the new token's K/V are
+    # quantized into the cache and attended along with it) needs 16-bit
+    # activations and group size 32/64/128; otherwise, or with --unfused, a
+    # layer takes three launches (quantize K, quantize V, attention).
+    fused = not args.unfused and w["dtype"] != "f32" and G in (32, 64, 128)
+
     def attn(layer):
+        if fused:
+            ops.decode_step(
+                layer["q"], layer["knew"], layer["vnew"], layer["kp"], layer["ks"], layer["vp"], layer["vs"],
+                pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm_scale, out=layer["out"],
+            )
+            return
         ops.fused_decode_attention(
             layer["q"], layer["kp"][:, :, :attended], layer["ks"][:, :, :attended],
             layer["vp"][:, :, :attended], layer["vs"][:, :, :attended],
@@ -169,8 +184,9 @@ def main() -> int:
 
     def step():
         for layer in layers:
-            ops.quantize_into(layer["knew"], layer["kp"], layer["ks"], G, pos)
-            ops.quantize_into(layer["vnew"], layer["vp"], layer["vs"], G, pos)
+            if not fused:
+                ops.quantize_into(layer["knew"], layer["kp"], layer["ks"], G, pos)
+                ops.quantize_into(layer["vnew"], layer["vp"], layer["vs"], G, pos)
             attn(layer)
 
     with torch.cuda.stream(stream):
@@ -254,7 +270,11 @@ def main() -> int:
     a_bytes = attn_bytes(w, kv_tokens)
     step_bytes = L * (a_bytes + append_bytes(w))
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    achieved = a_bytes / (attn_us * 1e-6) / 1e9
+    # bytes the measured launch moves: the fused step reads the cache's old
+    # rows (the new one comes from registers) plus the new K/V rows and writes
+    # their codes; the unfused attention launch reads every row
+    k_bytes = (attn_bytes(w, kv_tokens - B) + append_bytes(w)) if fused else a_bytes
+    achieved = k_bytes / (attn_us * 1e-6) / 1e9
 
     result = {
         "metric": METRIC,
@@ -272,7 +292,7 @@ def main() -> int:
         "config": {
             "workload": w["desc"], "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
             "group_size": G, "context": ctx, "layers": L, "ragged": w["ragged"],
-            "graph": graph is not None,
+            "graph": graph is not None, "fused_step": fused,
         },
         "ms_per_token": round(ms_per_step, 5),
         "attn_us_per_layer": round(attn_us, 3),
@@ -284,8 +304,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(args.traffic_summary, w),
-            "kernel": "decode_attn_mfma_kernel" if w["dtype"] != "f32" else "decode_attn_valu_kernel",
-            "bytes_per_launch": a_bytes,
+            "kernel": ("decode_attn_mfma_kernel (decode step: append + attention)" if fused else
+                       "decode_attn_mfma_kernel" if w["dtype"] != "f32" else "decode_attn_valu_kernel"),
+            "bytes_per_launch": k_bytes,
         },
     }
 

@@ -153,6 +153,47 @@ int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_strides,
                     int64_t n_split, void* workspace, int64_t workspace_bytes,
                     void* stream);
 
+/*
+ * kvq_decode_step — one decode token of one layer in one launch: quantize the
+ * new K and V rows and append them to the INT4 cache in place, then attend
+ * over the cache including them.
+ *
+ * Replaces, for Sq = 1, the pair the reference runs per layer and token:
+ * models/llama3/kv_cache.py:76-105 QuantizedKVCache.append (quantize_int4,
+ * kernels/llama3/quantize.py:189-207, then torch.cat) followed by
+ * kernels/llama3/attention_quant.py:159-286 attention_forward_quant_gqa
+ * (llama3_quant.py:62-88); codes and scales written are bit-identical to
+ * kvq_quantize's and the attention matches kvq_decode_attn over the appended
+ * cache.
+ *
+ * q:      [B, Hq, 1, D] (bf16 or fp16), element strides q_strides[4].
+ * k_new, v_new: [B, Hkv, 1, D] in q's dtype, element strides [4] with unit
+ *         inner stride and 4-byte aligned rows.
+ * k_packed/v_packed [B, Hkv, capacity, G*groups/2] uint8 and k_scales/
+ * v_scales [B, Hkv, capacity, groups] (16-bit scale_dtype), byte / element
+ * strides [3]: the cache buffers. Sequence b's old length is positions[b]
+ * (device int32 [B]) or pos0 for every sequence; its new row is written at
+ * that index and it attends old length + 1 keys. A sequence whose old length
+ * is not below `capacity` is left unchanged and attends its first `capacity`
+ * keys (pos0 is checked on the host).
+ * group_size in {32, 64, 128}; D in {64, 128}. n_split / workspace as for
+ * kvq_decode_attn (plan with s_max = the longest attended length).
+ */
+int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
+                    const void* k_new, const int64_t* kn_strides,
+                    const void* v_new, const int64_t* vn_strides,
+                    void* k_packed, const int64_t* kp_strides,
+                    void* k_scales, const int64_t* ks_strides,
+                    void* v_packed, const int64_t* vp_strides,
+                    void* v_scales, const int64_t* vs_strides,
+                    int scale_dtype,
+                    void* out, const int64_t* out_strides,
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                    int64_t group_size, int64_t capacity,
+                    const int32_t* positions, int64_t pos0, float sm_scale,
+                    int64_t n_split, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,13 @@ struct AttnArgs {
   int Hkv, Sq, G, Sk, ratio, rows_total, row_chunks, n_units;
   int n_split, causal, scale_dtype, xcd_remap, q_vec;
   float scale_log2;
+  // decode step (append != 0): the new token's K/V rows [B, Hkv, 1, D] (q's
+  // dtype, unit inner stride), quantized and written at each sequence's old
+  // length (seq_lens[b], or pos0 for all) and attended along with the cache
+  int append, pos0;
+  const void* knew;
+  const void* vnew;
+  int64_t kns_b, kns_h, vns_b, vns_h;
   uint32_t* ws_cnt;  // [n_units] arrival counters (zero between calls)
   float* ws_ml;      // [n_units][n_split][ROWS][2]  (max, sum)
   float* ws_o;       // [n_units][n_split][ROWS][D]
@@ -532,11 +539,13 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const int kvh = bh % a.Hkv;
   const int b = bh / a.Hkv;
 
-  int L = a.Sk;
-  if (a.seq_lens) {
-    const int sl = a.seq_lens[b];
-    L = sl < 0 ? 0 : (sl < a.Sk ? sl : a.Sk);
-  }
+  int L = a.append ? a.pos0 : a.Sk;
+  if (a.seq_lens) L = a.seq_lens[b];
+  L = L < 0 ? 0 : L;
+  // decode step: the new token goes to row L (if it fits the cache) and is
+  // attended by the unit's last split from registers
+  const bool has_new = a.append && L < a.Sk && split == a.n_split - 1;
+  L = L < a.Sk ? L : a.Sk;
   int t_begin, t_end;
   split_range(a, L, split, t_begin, t_end);
   // Tiles of 64 keys, dealt to the waves round-robin. A split of whole passes
@@ -674,6 +683,14 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     tail_ks = __builtin_amdgcn_raw_buffer_load_b16(rks, tt * kss2 + sg, 0, 0);
     tail_vs = __builtin_amdgcn_raw_buffer_load_b16(rvs, tt * vss2 + sg, 0, 0);
   }
+  // decode step: the last wave of the unit's last split holds the new
+  // token's K and V elements 2l, 2l+1 (lane l)
+  uint32_t new_k2 = 0u, new_v2 = 0u;
+  const bool new_here = has_new && wave == NW - 1;
+  if (new_here && lane < D / 2) {
+    new_k2 = *((const uint32_t*)((const uint16_t*)a.knew + (int64_t)b * a.kns_b + (int64_t)kvh * a.kns_h) + lane);
+    new_v2 = *((const uint32_t*)((const uint16_t*)a.vnew + (int64_t)b * a.vns_b + (int64_t)kvh * a.vns_h) + lane);
+  }
   // query rows -> this wave's LDS copy, permuted to the key operand order:
   // (e0,e2) (e1,e3) (e4,e6) (e5,e7) of every 8 elements
 #pragma unroll
@@ -708,6 +725,116 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       }
       qinit[rs][c] = acc;
     }
+  }
+
+  // ---- single keys outside the tile loop (a split's tail keys, a decode
+  //      step's new token): lane l owns dims 2l, 2l+1 (k0, k1, v0, v1:
+  //      dequantized fp32). key_scores gives s_r = q_r . k summed over the
+  //      wave (log2 units, masked rows kNeg); fold_in then makes the wave's
+  //      partial in LDS absorb the key: M = max(m, s), o = o 2^(m - M) +
+  //      v 2^(s - M), l = l 2^(m - M) + 2^(s - M). ----
+  const int lc = lane % (D / 2);
+  const bool col_ok = lane < D / 2;
+  auto key_scores = [&](float k0, float k1, int key, float (&st)[RS][4]) {
+    // query elements 2l, 2l+1 from the permuted copy: element pairs of each 8
+    // sit as (e0,e2) (e1,e3) (e4,e6) (e5,e7)
+    const int kd = lc / 4, jj = lc % 4;
+    const int dwa = 4 * kd + 2 * (jj >> 1);
+    const bool hi = (jj & 1) != 0;
+    k0 = col_ok ? k0 : 0.0f;
+    k1 = col_ok ? k1 : 0.0f;
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t qa = q_lds[wave][rs * 4 + r][dwa], qb = q_lds[wave][rs * 4 + r][dwa + 1];
+        const uint32_t ha = hi ? (qa >> 16) : (qa & 0xffffu), hb = hi ? (qb >> 16) : (qb & 0xffffu);
+        const float q0 = F16 ? f16_bits_to_f32(ha) : bf16_bits_to_f32(ha);
+        const float q1 = F16 ? f16_bits_to_f32(hb) : bf16_bits_to_f32(hb);
+        st[rs][r] = fmaf(q0, k0, q1 * k1);
+      }
+      float tot[4];
+      wave_reduce4<true>(st[rs], tot);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bool ok = true;
+        if constexpr (ROWMASK) ok = key < lim[rs][r];
+        st[rs][r] = ok ? tot[r] * a.scale_log2 : kNeg;
+      }
+    }
+  };
+  auto fold_in = [&](const float (&st)[RS][4], float v0, float v1) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = rs * 4 + r;
+        const float m_old = ml_lds[wave][row][0], l_old = ml_lds[wave][row][1];
+        const float sv = st[rs][r];
+        const float M = fmax_nc(m_old, sv);
+        const float fa = __builtin_amdgcn_exp2f(m_old - M);
+        const float fb = sv > kNeg ? __builtin_amdgcn_exp2f(sv - M) : 0.0f;
+        if (col_ok) {
+          const float2 o2 = *(const float2*)&o_lds[wave][row][2 * lc];
+          *(float2*)&o_lds[wave][row][2 * lc] = make_float2(fmaf(o2.x, fa, v0 * fb), fmaf(o2.y, fa, v1 * fb));
+        }
+        if (lane == 0) {
+          ml_lds[wave][row][0] = M;
+          ml_lds[wave][row][1] = fmaf(l_old, fa, fb);
+        }
+      }
+    }
+  };
+  // decode step: quantize the new K and V rows exactly as the quantize kernel
+  // does (group absmax / 7 in fp32, IEEE division, round half to even, clamp,
+  // +8; scale narrowed once for storage), store them at row L, and score the
+  // dequantized key (stored scale) now, while the tiles are in flight; the
+  // fold happens after the loop. Lane l owns code byte l of the packed row
+  // (packed width = groups x G/2 bytes <= 64).
+  float new_st[RS][4];
+  float new_v[2] = {0.0f, 0.0f};
+  if (new_here) {
+    const int G = a.G;
+    const int W = ((D + G - 1) / G) * (G / 2);
+    const bool byte_ok = lane < W;
+    float deq[2][2];
+#pragma unroll
+    for (int kvsel = 0; kvsel < 2; ++kvsel) {
+      const uint32_t x2 = kvsel == 0 ? new_k2 : new_v2;
+      const float x0 = col_ok ? (F16 ? f16_bits_to_f32(x2 & 0xffffu) : bf16_bits_to_f32(x2 & 0xffffu)) : 0.0f;
+      const float x1 = col_ok ? (F16 ? f16_bits_to_f32(x2 >> 16) : bf16_bits_to_f32(x2 >> 16)) : 0.0f;
+      // group absmax: G / 2 consecutive lanes (16, 32 or 64)
+      float am = row16_max(fmax_nc(fabsf(x0), fabsf(x1)));
+      if (G >= 64) {  // rows of 16 lanes pairwise: (0, 1), (2, 3)
+        float u = am, v = am;
+        permlane16_swap(u, v);
+        am = fmax_nc(u, v);
+      }
+      if (G >= 128) {  // halves of 32 lanes
+        float u = am, v = am;
+        permlane32_swap(u, v);
+        am = fmax_nc(u, v);
+      }
+      const float scale = am > 0.0f ? am / 7.0f : 1.0f;
+      float c0 = __builtin_rintf(x0 / scale), c1 = __builtin_rintf(x1 / scale);
+      c0 = fminf(fmaxf(c0, -8.0f), 7.0f);
+      c1 = fminf(fmaxf(c1, -8.0f), 7.0f);
+      const uint32_t byte = (uint32_t)((int)c0 + 8) | ((uint32_t)((int)c1 + 8) << 4);
+      const uint32_t sbits = S_F16 ? f32_to_f16_bits(scale) : f32_to_bf16_bits(scale);
+      uint8_t* prow = const_cast<uint8_t*>(kvsel == 0 ? kp_bh : vp_bh) + (int64_t)L * (kvsel == 0 ? kps : vps);
+      uint16_t* srow = const_cast<uint16_t*>(kvsel == 0 ? ks_bh : vs_bh) + (int64_t)L * (kvsel == 0 ? a.kss_s : a.vss_s);
+      if (byte_ok) prow[lane] = (uint8_t)byte;
+      if (byte_ok && (2 * lane) % G == 0) srow[(2 * lane) / G] = (uint16_t)sbits;
+      const float sq = scale16_to_f32(sbits, S_F16);
+      deq[kvsel][0] = c0 * sq;
+      deq[kvsel][1] = c1 * sq;
+    }
+    key_scores(deq[0][0], deq[0][1], L, new_st);
+    new_v[0] = deq[1][0];
+    new_v[1] = deq[1][1];
   }
 
   // ---- running softmax state (base 2; scores carry sm_scale * log2 e) ----
@@ -942,65 +1069,17 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       }
     }
   }
-  // ---- tail key of this wave: score s_r = q_r . k (lanes own dims 2l, 2l+1,
-  //      summed over the wave), then the wave's partial absorbs it:
-  //      M = max(m, s), o = o 2^(m - M) + v 2^(s - M), l = l 2^(m - M) + 2^(s - M) ----
+  // ---- extra keys folded into this wave's partial (already in LDS): the
+  //      split's tail key of this wave and, in a decode step, the new token
+  //      (scored before the tile loop). ----
   if (wave < n_tail) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const bool col_ok = lane < D / 2;
     const float ksf = scale16_to_f32(tail_ks, S_F16), vsf = scale16_to_f32(tail_vs, S_F16);
-    const float k0 = col_ok ? ((float)(int)(tail_kb & 15u) - 8.0f) * ksf : 0.0f;
-    const float k1 = col_ok ? ((float)(int)((tail_kb >> 4) & 15u) - 8.0f) * ksf : 0.0f;
-    const float v0 = ((float)(int)(tail_vb & 15u) - 8.0f) * vsf;
-    const float v1 = ((float)(int)((tail_vb >> 4) & 15u) - 8.0f) * vsf;
-    // query elements 2l, 2l+1 from the permuted copy: element pairs of each 8
-    // sit as (e0,e2) (e1,e3) (e4,e6) (e5,e7)
-    const int lc = lane % (D / 2), kd = lc / 4, jj = lc % 4;
-    const int dwa = 4 * kd + 2 * (jj >> 1);
-    const bool hi = (jj & 1) != 0;
     float st[RS][4];
-#pragma unroll
-    for (int rs = 0; rs < RS; ++rs) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t qa = q_lds[wave][rs * 4 + r][dwa], qb = q_lds[wave][rs * 4 + r][dwa + 1];
-        const uint32_t ha = hi ? (qa >> 16) : (qa & 0xffffu), hb = hi ? (qb >> 16) : (qb & 0xffffu);
-        const float q0 = F16 ? f16_bits_to_f32(ha) : bf16_bits_to_f32(ha);
-        const float q1 = F16 ? f16_bits_to_f32(hb) : bf16_bits_to_f32(hb);
-        st[rs][r] = fmaf(q0, k0, q1 * k1);
-      }
-      float tot[4];
-      wave_reduce4<true>(st[rs], tot);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bool ok = true;
-        if constexpr (ROWMASK) ok = tail_t < lim[rs][r];
-        st[rs][r] = ok ? tot[r] * a.scale_log2 : kNeg;
-      }
-    }
-#pragma unroll
-    for (int rs = 0; rs < RS; ++rs) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = rs * 4 + r;
-        const float m_old = ml_lds[wave][row][0], l_old = ml_lds[wave][row][1];
-        const float sv = st[rs][r];
-        const float M = fmax_nc(m_old, sv);
-        const float fa = __builtin_amdgcn_exp2f(m_old - M);
-        const float fb = sv > kNeg ? __builtin_amdgcn_exp2f(sv - M) : 0.0f;
-        if (col_ok) {
-          const float2 o2 = *(const float2*)&o_lds[wave][row][2 * lc];
-          *(float2*)&o_lds[wave][row][2 * lc] = make_float2(fmaf(o2.x, fa, v0 * fb), fmaf(o2.y, fa, v1 * fb));
-        }
-        if (lane == 0) {
-          ml_lds[wave][row][0] = M;
-          ml_lds[wave][row][1] = fmaf(l_old, fa, fb);
-        }
-      }
-    }
+    key_scores(((float)(int)(tail_kb & 15u) - 8.0f) * ksf, ((float)(int)((tail_kb >> 4) & 15u) - 8.0f) * ksf,
+               tail_t, st);
+    fold_in(st, ((float)(int)(tail_vb & 15u) - 8.0f) * vsf, ((float)(int)((tail_vb >> 4) & 15u) - 8.0f) * vsf);
   }
+  if (new_here) fold_in(new_st, new_v[0], new_v[1]);
   __syncthreads();
   finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
 }
@@ -1460,7 +1539,16 @@ extern "C" int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_
   return workspace_bytes_for(p, D);
 }
 
-extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_strides,
+// Decode-step extras: the new token's K/V rows and where they go.
+struct StepArgs {
+  const void* knew;
+  const int64_t* kn_strides;
+  const void* vnew;
+  const int64_t* vn_strides;
+  int64_t pos0;
+};
+
+static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides,
                                const void* k_packed, const int64_t* kp_strides,
                                const void* k_scales, const int64_t* ks_strides,
                                const void* v_packed, const int64_t* vp_strides,
@@ -1471,8 +1559,7 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
                                int64_t group_size, int64_t Sk,
                                const int32_t* seq_lens, int is_causal, float sm_scale,
                                int64_t n_split, void* workspace, int64_t workspace_bytes,
-                               void* stream) {
-  clear_error();
+                               void* stream, const StepArgs* step) {
   KVQ_CHECK_ARG(dtype_ok(q_dtype), "kvq_decode_attn: q dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_decode_attn: scale dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(q_strides && kp_strides && ks_strides && vp_strides && vs_strides && out_strides,
@@ -1565,6 +1652,12 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   a.q_vec = (q_dtype != KVQ_F32 && q_strides[3] == 1 && (uintptr_t)q % 16 == 0 &&
              q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 && q_strides[2] % 8 == 0) ? 1 : 0;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.append = step ? 1 : 0;
+  a.pos0 = step ? (int)step->pos0 : 0;
+  a.knew = step ? step->knew : nullptr;
+  a.vnew = step ? step->vnew : nullptr;
+  a.kns_b = step ? step->kn_strides[0] : 0; a.kns_h = step ? step->kn_strides[1] : 0;
+  a.vns_b = step ? step->vn_strides[0] : 0; a.vns_h = step ? step->vn_strides[1] : 0;
   a.ws_cnt = nullptr; a.ws_ml = nullptr; a.ws_o = nullptr;
   if (need > 0) {
     char* w = (char*)workspace;
@@ -1579,4 +1672,65 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   else launch_d<64>(a, p, q_dtype, rowmask, grid, st);
   KVQ_CHECK_LAUNCH("kvq_decode_attn");
   return KVQ_OK;
+}
+
+extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_strides,
+                               const void* k_packed, const int64_t* kp_strides,
+                               const void* k_scales, const int64_t* ks_strides,
+                               const void* v_packed, const int64_t* vp_strides,
+                               const void* v_scales, const int64_t* vs_strides,
+                               int scale_dtype,
+                               void* out, const int64_t* out_strides,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                               int64_t group_size, int64_t Sk,
+                               const int32_t* seq_lens, int is_causal, float sm_scale,
+                               int64_t n_split, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  clear_error();
+  return decode_attn_impl(q, q_dtype, q_strides, k_packed, kp_strides, k_scales, ks_strides, v_packed,
+                          vp_strides, v_scales, vs_strides, scale_dtype, out, out_strides, B, Hq, Hkv, Sq,
+                          D, group_size, Sk, seq_lens, is_causal, sm_scale, n_split, workspace,
+                          workspace_bytes, stream, nullptr);
+}
+
+extern "C" int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
+                               const void* k_new, const int64_t* kn_strides,
+                               const void* v_new, const int64_t* vn_strides,
+                               void* k_packed, const int64_t* kp_strides,
+                               void* k_scales, const int64_t* ks_strides,
+                               void* v_packed, const int64_t* vp_strides,
+                               void* v_scales, const int64_t* vs_strides,
+                               int scale_dtype,
+                               void* out, const int64_t* out_strides,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                               int64_t group_size, int64_t capacity,
+                               const int32_t* positions, int64_t pos0, float sm_scale,
+                               int64_t n_split, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(dtype_ok(q_dtype) && dtype_ok(scale_dtype), "kvq_decode_step: bad dtype");
+  KVQ_CHECK_ARG(kn_strides && vn_strides && q_strides, "kvq_decode_step: null stride array");
+  if (!use_mfma(q_dtype, scale_dtype) || !(group_size == 32 || group_size == 64 || group_size == 128)) {
+    set_error("kvq_decode_step: needs bf16/fp16 queries, 16-bit scales and group_size in {32, 64, 128}");
+    return KVQ_EUNSUP;
+  }
+  KVQ_CHECK_ARG(capacity >= 1, "kvq_decode_step: capacity must be >= 1");
+  KVQ_CHECK_ARG(positions != nullptr || (pos0 >= 0 && pos0 < capacity),
+                "kvq_decode_step: write position %lld outside the cache capacity %lld", (long long)pos0,
+                (long long)capacity);
+  if (B == 0) return KVQ_OK;
+  KVQ_CHECK_ARG(k_new && v_new, "kvq_decode_step: null new K/V");
+  const bool kn_ok = kn_strides[3] == 1 && (uintptr_t)k_new % 4 == 0 && kn_strides[0] % 2 == 0 &&
+                     kn_strides[1] % 2 == 0;
+  const bool vn_ok = vn_strides[3] == 1 && (uintptr_t)v_new % 4 == 0 && vn_strides[0] % 2 == 0 &&
+                     vn_strides[1] % 2 == 0;
+  if (!kn_ok || !vn_ok) {
+    set_error("kvq_decode_step: new K/V rows need unit inner stride and 4-byte alignment");
+    return KVQ_EUNSUP;
+  }
+  const StepArgs step{k_new, kn_strides, v_new, vn_strides, pos0};
+  return decode_attn_impl(q, q_dtype, q_strides, k_packed, kp_strides, k_scales, ks_strides, v_packed,
+                          vp_strides, v_scales, vs_strides, scale_dtype, out, out_strides, B, Hq, Hkv, 1,
+                          D, group_size, capacity, positions, 0, sm_scale, n_split, workspace,
+                          workspace_bytes, stream, &step);
 }

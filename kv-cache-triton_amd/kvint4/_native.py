@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_attn_num_splits",
     "kvq_decode_attn_workspace_bytes",
     "kvq_decode_attn",
+    "kvq_decode_step",
 )
 
 _lock = threading.Lock()
@@ -72,6 +73,17 @@ def _declare(lib: ctypes.CDLL) -> None:
         _vp, _i64p,
         _i64, _i64, _i64, _i64, _i64, _i64, _i64,
         _vp, _i32, ctypes.c_float,
+        _i64, _vp, _i64, _vp,
+    ]
+    lib.kvq_decode_step.restype = _i32
+    lib.kvq_decode_step.argtypes = [
+        _vp, _i32, _i64p,
+        _vp, _i64p, _vp, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _i32,
+        _vp, _i64p,
+        _i64, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, ctypes.c_float,
         _i64, _vp, _i64, _vp,
     ]
 

@@ -25,7 +25,7 @@ from typing import Optional
 
 import torch
 
-from . import ops
+from . import _native, ops
 
 _ROUND = 256  # capacity granularity (tokens)
 
@@ -152,6 +152,47 @@ class QuantizedKVCacheBase:
     def append(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> None:
         """Quantize [B, H_kv, S, d] K/V and append them to layer `layer_idx`."""
         self._append_quantized(key_states, value_states, layer_idx)
+
+    def append_and_attend(
+        self,
+        query_states: torch.Tensor,
+        key_states: torch.Tensor,
+        value_states: torch.Tensor,
+        layer_idx: int,
+        *,
+        n_kv_heads: int,
+        scale: float,
+    ) -> Optional[torch.Tensor]:
+        """Decode fast path: one kernel launch quantizes the new token's K/V
+        [B, H_kv, 1, d] into the layer's buffers (in place) and attends
+        query_states [B, H_q, 1, d] over the cache including it; the same
+        result as ``append`` followed by fused attention over
+        ``get_quantized``. Returns None, with the cache untouched, when the
+        fused step does not apply (not one decode token, an empty layer, or a
+        dtype / group size it does not handle); the caller then appends and
+        attends separately."""
+        if query_states.shape[2] != 1 or key_states.shape[2] != 1 or not query_states.is_cuda:
+            return None
+        if key_states.shape != value_states.shape or key_states.dim() != 4:
+            return None
+        prev = self._layers.get(layer_idx)
+        if prev is None or prev.seq_len == 0:
+            return None
+        start = prev.seq_len
+        layer = self._ensure_layer(key_states, layer_idx, start + 1)
+        pos = layer.seq_lens if layer.seq_lens is not None else start
+        try:
+            out = ops.decode_step(
+                query_states, key_states, value_states,
+                layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales, pos,
+                n_kv_heads=n_kv_heads, group_size=self.group_size, sm_scale=scale,
+            )
+        except _native.KVQUnsupported:
+            return None
+        if layer.seq_lens is not None:
+            layer.seq_lens.add_(1)
+        layer.seq_len = start + 1
+        return out
 
     def load_ragged(
         self,

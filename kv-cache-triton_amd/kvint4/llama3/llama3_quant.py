@@ -4,7 +4,9 @@ Drop-in for ``models/llama3/llama3_quant.py`` (:36-204):
 
     hidden_states -> q_proj / k_proj / v_proj -> [B, n, S, d] -> RoPE(q, k)
     if past_key_values is a kvint4 QuantizedKVCache:
-        cache.append(k, v)  (HIP quantize, written in place)
+        decode token, no mask -> cache.append_and_attend: one HIP launch
+                    quantizes the new K/V into the cache and attends over it
+        otherwise: cache.append(k, v)  (HIP quantize, written in place)
         no mask  -> attention_forward_quant_gqa over the packed cache
                     (decode: fused split-K kernel; prefill: HIP dequant + SDPA)
         mask     -> dequantize the cache, HF attention interface with the mask
@@ -64,6 +66,15 @@ class LlamaAttentionQuantized(LlamaAttention):
 
         if isinstance(past_key_values, QuantizedKVCache):
             cache = past_key_values
+            if attention_mask is None and query_states.shape[-2] == 1:
+                # decode: append + attention in one launch
+                attn_output = cache.append_and_attend(
+                    query_states, key_states, value_states, self.layer_idx,
+                    n_kv_heads=self.config.num_key_value_heads, scale=self.scaling,
+                )
+                if attn_output is not None:
+                    attn_output = attn_output.transpose(1, 2).reshape(*input_shape, -1).contiguous()
+                    return self.o_proj(attn_output), None
             cache.append(key_states, value_states, self.layer_idx)
             if attention_mask is None:
                 k_packed, k_scales, v_packed, v_scales = cache.get_quantized(self.layer_idx)

@@ -286,6 +286,84 @@ def fused_decode_attention(
     return out
 
 
+def decode_step(
+    q: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_packed: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_packed: torch.Tensor,
+    v_scales: torch.Tensor,
+    position,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    sm_scale: float,
+    out: torch.Tensor | None = None,
+    n_split: int | None = None,
+) -> torch.Tensor:
+    """One decode token in one launch: quantize k_new / v_new [B, Hkv, 1, D]
+    into row `position` of the capacity buffers (an int for every sequence, or
+    a device int32 [B] of per-sequence old lengths) and attend q [B, Hq, 1, D]
+    over the cache including the new row. The buffers are the cache's
+    [B, Hkv, capacity, .] tensors, written in place; the caller advances its
+    lengths. Raises KVQUnsupported for dtype/group combinations the fused
+    step does not handle (the caller then quantizes and attends separately)."""
+    B, Hq, Sq, D = q.shape
+    if Sq != 1:
+        raise nat.KVQUnsupported("decode_step handles one query position")
+    cap = int(k_packed.shape[2])
+    if out is None:
+        out = torch.empty_like(q)
+    if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+        raise nat.KVQUnsupported("decode_step needs K/V rows in q's dtype")
+    if k_new.stride(-1) != 1:
+        k_new = k_new.contiguous()
+    if v_new.stride(-1) != 1:
+        v_new = v_new.contiguous()
+    lib = nat.lib()
+    qd = nat.DTYPE_CODE[q.dtype]
+    sd = nat.DTYPE_CODE[k_scales.dtype]
+    if isinstance(position, torch.Tensor):
+        if position.dtype != torch.int32 or not position.is_cuda or position.numel() != B:
+            raise ValueError("position must be an int or a device int32 tensor of shape [B]")
+        pos_ptr, pos0, s_max = position.contiguous().data_ptr(), 0, cap
+    else:
+        pos_ptr, pos0 = None, int(position)
+        if not 0 <= pos0 < cap:
+            raise ValueError(f"write position {pos0} outside the cache capacity {cap}")
+        s_max = pos0 + 1
+    if n_split is None:
+        n_split = lib.kvq_decode_attn_num_splits(B, Hq, n_kv_heads, 1, D, s_max, qd, sd, _num_cus(q.device))
+        if n_split < 0:
+            nat.check(int(n_split), "kvq_decode_attn_num_splits")
+    ws_bytes = lib.kvq_decode_attn_workspace_bytes(B, Hq, n_kv_heads, 1, D, qd, sd, n_split)
+    if ws_bytes < 0:
+        nat.check(int(ws_bytes), "kvq_decode_attn_workspace_bytes")
+    with nat.device_of(q):
+        stream = nat.stream_handle(q.device)
+        ws_ptr, ws_len = None, 0
+        if ws_bytes > 0:
+            ws = _workspaces.get(q.device, stream, ws_bytes)
+            ws_ptr, ws_len = ws.data_ptr(), ws.numel()
+        rc = lib.kvq_decode_step(
+            q.data_ptr(), qd, nat.i64_array(q.stride()),
+            k_new.data_ptr(), nat.i64_array(k_new.stride()),
+            v_new.data_ptr(), nat.i64_array(v_new.stride()),
+            k_packed.data_ptr(), nat.i64_array(k_packed.stride()[:3]),
+            k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:3]),
+            v_packed.data_ptr(), nat.i64_array(v_packed.stride()[:3]),
+            v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:3]),
+            sd,
+            out.data_ptr(), nat.i64_array(out.stride()),
+            B, Hq, n_kv_heads, D, group_size, cap,
+            pos_ptr, pos0, float(sm_scale),
+            n_split, ws_ptr, ws_len, stream,
+        )
+    nat.check(rc, "kvq_decode_step")
+    return out
+
+
 def _sdpa_dense(q, k, v, *, is_causal: bool, sm_scale: float, attn_mask=None) -> torch.Tensor:
     """Dense attention on already-dequantized, GQA-expanded K/V.
 

@@ -1,0 +1,143 @@
+"""Fused decode step (kvq_decode_step): quantize-append of the new token and
+decode attention in one launch, against the two-launch path it replaces
+(quantize_into + fused attention over the appended cache; reference
+models/llama3/kv_cache.py:76-105 then kernels/llama3/attention_quant.py:159-286)
+and against the float64 oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from kvint4 import ops
+from oracle import kvq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TDT = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _cache(B, Hkv, cap, D, G, dtype, n_fill, seed):
+    g = torch.Generator().manual_seed(seed)
+    t, sdt = TDT[dtype], TDT[dtype]
+    W, NG = ops.packed_width(D, G), ops.num_groups(D, G)
+    kp = torch.zeros(B, Hkv, cap, W, dtype=torch.uint8, device=DEV)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(B, Hkv, cap, NG, dtype=sdt, device=DEV)
+    vs = torch.zeros_like(ks)
+    if n_fill:
+        k = torch.randn(B, Hkv, n_fill, D, generator=g).to(t).to(DEV)
+        v = torch.randn(B, Hkv, n_fill, D, generator=g).to(t).to(DEV)
+        ops.quantize_into(k, kp, ks, G, 0)
+        ops.quantize_into(v, vp, vs, G, 0)
+    return [kp, ks, vp, vs]
+
+
+def _close(got, want):
+    """Same attention, the new key folded in fp32 instead of through the
+    matrix-core PV product, whose softmax weights are rounded to bf16 (2^-9
+    relative). With few keys the weighted values can cancel, so the bound is
+    absolute: 2^-6 (about 2^-9 times the largest |v| of these inputs, 8
+    times) plus one bf16 unit in the last place of the output."""
+    g, w = got.float().cpu().numpy(), want.float().cpu().numpy()
+    assert np.all(np.abs(g - w) <= 2.0 ** -6 + 2.0 ** -7 * np.abs(w)), np.abs(g - w).max()
+
+
+def _new(B, Hq, Hkv, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed + 1000)
+    t = TDT[dtype]
+    q = torch.randn(B, Hq, 1, D, generator=g).to(t).to(DEV)
+    kn = (3.0 * torch.randn(B, Hkv, 1, D, generator=g)).to(t).to(DEV)
+    vn = torch.randn(B, Hkv, 1, D, generator=g).to(t).to(DEV)
+    return q, kn, vn
+
+
+CASES = [
+    # B, Hq, Hkv, D, G, pos, dtype
+    (1, 32, 8, 128, 32, 16384, "bf16"),  # north-star shape
+    (1, 32, 8, 128, 32, 4096, "bf16"),
+    (1, 32, 8, 128, 32, 1, "bf16"),
+    (1, 32, 8, 128, 32, 300, "bf16"),
+    (2, 64, 8, 128, 32, 2000, "bf16"),   # 8 query rows per KV head
+    (1, 8, 2, 128, 64, 777, "bf16"),
+    (1, 8, 2, 128, 128, 513, "bf16"),
+    (2, 12, 12, 64, 32, 1023, "f16"),    # GPT-2 shape (MHA, fp16 scales)
+    (1, 16, 4, 64, 64, 100, "f16"),
+    (1, 4, 4, 64, 128, 65, "f16"),       # G > D: padded group
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,G,pos,dtype", CASES)
+def test_decode_step_matches_append_then_attend(B, Hq, Hkv, D, G, pos, dtype):
+    cap = pos + 8
+    a = _cache(B, Hkv, cap, D, G, dtype, pos, seed=pos + D)
+    b = [t.clone() for t in a]
+    q, kn, vn = _new(B, Hq, Hkv, D, dtype, seed=pos)
+    sm = D ** -0.5
+    # two-launch path
+    ops.quantize_into(kn, a[0], a[1], G, pos)
+    ops.quantize_into(vn, a[2], a[3], G, pos)
+    n = pos + 1
+    want = ops.fused_decode_attention(q, a[0][:, :, :n], a[1][:, :, :n], a[2][:, :, :n], a[3][:, :, :n],
+                                      n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm)
+    # one launch
+    got = ops.decode_step(q, kn, vn, b[0], b[1], b[2], b[3], pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):  # the whole buffers: new row bit-identical, nothing else touched
+        assert torch.equal(x, y)
+    exact = O.attention_over_quantized(
+        q.float().cpu().numpy(), a[0][:, :, :n].cpu().numpy(), a[1][:, :, :n].float().cpu().numpy(),
+        a[2][:, :, :n].cpu().numpy(), a[3][:, :, :n].float().cpu().numpy(), group_size=G, scale=sm)
+    assert np.abs(got.float().cpu().numpy() - exact).max() <= 2e-2
+    _close(got, want)
+
+
+def test_decode_step_ragged_positions():
+    B, Hq, Hkv, D, G = 4, 32, 8, 128, 32
+    cap = 1200
+    a = _cache(B, Hkv, cap, D, G, "bf16", 1100, seed=7)
+    b = [t.clone() for t in a]
+    pos = torch.tensor([1100, 0, 517, 1], dtype=torch.int32, device=DEV)
+    q, kn, vn = _new(B, Hq, Hkv, D, "bf16", seed=7)
+    sm = D ** -0.5
+    ops.quantize_into(kn, a[0], a[1], G, pos)
+    ops.quantize_into(vn, a[2], a[3], G, pos)
+    want = ops.fused_decode_attention(q, a[0], a[1], a[2], a[3], n_kv_heads=Hkv, group_size=G,
+                                      is_causal=False, sm_scale=sm, seq_lens=pos + 1)
+    got = ops.decode_step(q, kn, vn, b[0], b[1], b[2], b[3], pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    _close(got, want)
+
+
+def test_decode_step_position_past_capacity_leaves_row():
+    """A sequence whose old length already fills the buffers is not written
+    and attends the keys it has."""
+    B, Hq, Hkv, D, G = 2, 32, 8, 128, 32
+    cap = 600
+    a = _cache(B, Hkv, cap, D, G, "bf16", cap, seed=11)
+    before = [t.clone() for t in a]
+    pos = torch.tensor([cap, 300], dtype=torch.int32, device=DEV)
+    q, kn, vn = _new(B, Hq, Hkv, D, "bf16", seed=11)
+    sm = D ** -0.5
+    got = ops.decode_step(q, kn, vn, a[0], a[1], a[2], a[3], pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    torch.cuda.synchronize()
+    for x, y in zip(a, before):
+        assert torch.equal(x[0], y[0])          # sequence 0 untouched
+        assert torch.equal(x[1, :, :300], y[1, :, :300])
+        assert torch.equal(x[1, :, 301:], y[1, :, 301:])
+    want0 = ops.fused_decode_attention(q[:1], a[0][:1], a[1][:1], a[2][:1], a[3][:1], n_kv_heads=Hkv,
+                                       group_size=G, is_causal=False, sm_scale=sm)
+    _close(got[:1], want0)
+
+
+def test_decode_step_rejects_bad_position_and_unsupported():
+    B, Hq, Hkv, D, G = 1, 8, 2, 128, 32
+    a = _cache(B, Hkv, 64, D, G, "bf16", 10, seed=3)
+    q, kn, vn = _new(B, Hq, Hkv, D, "bf16", seed=3)
+    with pytest.raises(ValueError):
+        ops.decode_step(q, kn, vn, *a, 64, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
+    with pytest.raises(ops.nat.KVQUnsupported):
+        ops.decode_step(q.float(), kn.float(), vn.float(), *a, 10, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
