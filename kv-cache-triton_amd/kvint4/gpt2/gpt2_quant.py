@@ -4,6 +4,8 @@ Drop-in for ``models/gpt2/gpt2_quant.py`` (:16-157), written against
 transformers 5.x ``GPT2Attention.forward``. Self-attention with a kvint4
 ``QuantizedKVCache`` appends through the HIP quantizer and attends over the
 packed cache:
+  * decode token, no mask, 16-bit activations -> ``append_and_attend``: one
+    HIP launch quantizes the new K/V into the cache and attends over it;
   * no mask -> ``attention_forward_quant`` (decode: fused kernel; prefill:
     HIP dequant + SDPA), scaled by the module's ``scaling``;
   * mask present -> dequantized cache through the HF attention interface.
@@ -63,10 +65,21 @@ class GPT2AttentionQuantized(GPT2Attention):
         shape_q = (*query_states.shape[:-1], -1, self.head_dim)
         query_states = query_states.view(shape_q).transpose(1, 2)
 
-        quant_cache.append(key_states, value_states, self.layer_idx)
-
         using_eager = self.config._attn_implementation == "eager"
-        if using_eager and self.reorder_and_upcast_attn:
+        fused_out = None
+        if attention_mask is None and query_states.shape[-2] == 1 and not (using_eager and self.reorder_and_upcast_attn):
+            # decode token: append + attention in one launch (16-bit models)
+            fused_out = quant_cache.append_and_attend(
+                query_states, key_states, value_states, self.layer_idx,
+                n_kv_heads=query_states.shape[1], scale=self.scaling,
+            )
+        if fused_out is None:
+            quant_cache.append(key_states, value_states, self.layer_idx)
+
+        if fused_out is not None:
+            attn_output = fused_out.transpose(1, 2)
+            attn_weights = None
+        elif using_eager and self.reorder_and_upcast_attn:
             k_full, v_full = quant_cache.get_dequantized(self.layer_idx)
             attn_output, attn_weights = self._upcast_and_reordered_attn(
                 query_states, k_full.to(query_states.dtype), v_full.to(query_states.dtype), attention_mask

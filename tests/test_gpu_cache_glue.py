@@ -26,6 +26,7 @@ from transformers.cache_utils import DynamicCache
 
 from kvint4.gpt2.gpt2_quant import replace_gpt2_attention_with_quantized
 from kvint4.gpt2.kv_cache import QuantizedKVCache as GPT2Cache
+from kvint4.llama3.attention_quant import attention_forward_quant_gqa
 from kvint4.llama3.kv_cache import QuantizedKVCache
 from kvint4.llama3.llama3_quant import LlamaAttentionQuantized, replace_llama_attention_with_quantized
 from oracle import kvq_oracle as O
@@ -181,3 +182,65 @@ def test_gpt2_random_init_decode_matches_reference():
             lq = quant(input_ids=nid, past_key_values=cq, use_cache=True).logits[:, -1]
             assert (lr - lq).abs().max().item() < 2.0
     assert cq.get_seq_length(0) == 26
+
+
+def test_cache_append_and_attend_matches_append_then_attend():
+    """QuantizedKVCache.append_and_attend (one launch) leaves the same cache
+    as append and gives the attention over it, for a uniform and a ragged layer."""
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, D = 2, 16, 4, 128
+    k0 = torch.randn(B, Hkv, 300, D, generator=g).to(torch.bfloat16).to(DEV)
+    v0 = torch.randn(B, Hkv, 300, D, generator=g).to(torch.bfloat16).to(DEV)
+    lens = torch.tensor([300, 123], dtype=torch.int32)
+    for ragged in (False, True):
+        ca, cb = QuantizedKVCache(group_size=32), QuantizedKVCache(group_size=32)
+        for c in (ca, cb):
+            if ragged:
+                c.load_ragged(k0, v0, 0, lens)
+            else:
+                c.append(k0, v0, 0)
+        for step in range(3):
+            q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+            kn = torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+            vn = torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+            got = cb.append_and_attend(q, kn, vn, 0, n_kv_heads=Hkv, scale=D ** -0.5)
+            assert got is not None
+            ca.append(kn, vn, 0)
+            kp, ks, vp, vs = ca.get_quantized(0)
+            want = attention_forward_quant_gqa(q, kp, ks, vp, vs, n_q_heads=Hq, n_kv_heads=Hkv,
+                                               scale=D ** -0.5, seq_lens=ca.get_seq_lens(0))
+            # Rows a ragged sequence has not written yet are uninitialised
+            # capacity in both caches: compare each sequence's own rows.
+            valid = [int(n) + step + 1 for n in lens] if ragged else [301 + step] * B
+            for i, (x, y) in enumerate(zip(ca.get_quantized(0), cb.get_quantized(0))):
+                for b in range(B):
+                    assert torch.equal(x[b, :, :valid[b]], y[b, :, :valid[b]]), (ragged, step, i, b)
+            assert ca.get_seq_length(0) == cb.get_seq_length(0) == 301 + step
+            if ragged:
+                assert torch.equal(ca.get_seq_lens(0), cb.get_seq_lens(0))
+            err = (got.float() - want.float()).abs().max().item()
+            assert err <= 2.0 ** -5, err
+
+
+def test_gpt2_fp16_decode_through_fused_step_matches_reference():
+    cfg = GPT2Config(n_layer=2, n_head=4, n_embd=256, vocab_size=256, n_positions=256)
+    torch.manual_seed(0)
+    ref = GPT2LMHeadModel(cfg).eval()                       # fp32, DynamicCache
+    quant = GPT2LMHeadModel(cfg).eval()
+    quant.load_state_dict(ref.state_dict())
+    use_fp32_reference_attention(ref)
+    replace_gpt2_attention_with_quantized(quant)
+    ref, quant = ref.to(DEV), quant.to(DEV).half()
+    torch.manual_seed(9)
+    prompt = torch.randint(0, 256, (1, 30), device=DEV)
+    with torch.no_grad():
+        cr, cq = DynamicCache(), GPT2Cache()
+        lr = ref(input_ids=prompt, past_key_values=cr, use_cache=True).logits[:, -1]
+        lq = quant(input_ids=prompt, past_key_values=cq, use_cache=True).logits[:, -1].float()
+        assert (lr - lq).abs().max().item() < 1.0 and lr.argmax().item() == lq.argmax().item()
+        for _ in range(6):
+            nid = torch.randint(0, 256, (1, 1), device=DEV)
+            lr = ref(input_ids=nid, past_key_values=cr, use_cache=True).logits[:, -1]
+            lq = quant(input_ids=nid, past_key_values=cq, use_cache=True).logits[:, -1].float()
+            assert (lr - lq).abs().max().item() < 2.0
+    assert cq.get_seq_length(0) == 36 and cq.get_quantized(0)[1].dtype == torch.float16
