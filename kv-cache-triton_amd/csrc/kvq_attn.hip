@@ -13,9 +13,11 @@
 // balanced to the token (split s of a sequence of L keys covers
 // [s*L/n_split, (s+1)*L/n_split)), so ragged batches stay balanced too. Partial
 // (max, sum, o) triples are merged across the waves of a workgroup in LDS and
-// then across splits by the last workgroup of the unit to finish (device-scope
-// release fence + atomic counter, acquire fence), which writes the output and
-// re-arms the counter.
+// then across splits by the last workgroup of the unit to finish (partials
+// stored and loaded with the device-coherent sc1 policy, arrival counted by
+// atomics), which writes the output and re-arms the counters. In a decode step
+// the same launch also quantizes the new token's K/V into the cache row after
+// the last one, and the unit's last split attends it from registers.
 //
 // Two kernels share that frame:
 //
@@ -72,7 +74,8 @@ struct AttnArgs {
   const void* knew;
   const void* vnew;
   int64_t kns_b, kns_h, vns_b, vns_h;
-  uint32_t* ws_cnt;  // [n_units] arrival counters (zero between calls)
+  uint32_t* ws_cnt;  // [kCntUnits][kSubCnt + 1] arrival counters, kCntStride
+                     // words apart (zero between calls)
   float* ws_ml;      // [n_units][n_split][ROWS][2]  (max, sum)
   float* ws_o;       // [n_units][n_split][ROWS][D]
 };
@@ -421,7 +424,8 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
 // hi = (w >> 4) & 0x0F0F0F0F (elements 1,3,5,7), perm(MAGIC, lo, sel) builds
 // {0x43 | lo.byte_i, 0x43 | lo.byte_j} pairs = bf16(128 + n) (fp16: 0x64 ->
 // 1024 + n). Key dword k therefore feeds the MFMA k-order (0,2,1,3) and
-// (4,6,5,7); each lane's query row is held in registers permuted the same way.
+// (4,6,5,7); the query rows, read from a wave-private LDS copy, are laid out
+// the same way.
 
 // Row max / row sum over a wave for the four values x[0..3] a lane holds for
 // one row set (one per query row). Two swap steps (lanes 32 apart, then rows
