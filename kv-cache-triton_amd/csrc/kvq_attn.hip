@@ -82,6 +82,7 @@ struct AttnArgs {
 
 constexpr float kNeg = -1.0e30f;
 constexpr int kMaxSplit = 64;  // split-K fan-out cap (bounds the merge's LDS)
+constexpr float kLazyMax = 8.0f;  // running-max slack of the MFMA kernel (log2 units)
 constexpr int kSubCnt = 4;      // arrival sub-counters per unit
 constexpr int kCntStride = 16;  // uint32 words between counters (64 bytes)
 constexpr uint32_t kNibPairs = 0x000F000Fu;
@@ -278,23 +279,27 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
       mv[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
                                             rm, (sp * ROWS + r) * 8u, 0, kSc1));
     }
+    // Straight-line fold (no branch per split, so every load above is in
+    // flight before the first wait): splits past the last read as zero
+    // (o = 0, l = 0) and take max kNeg, so they add nothing.
+    float mj[BATCH];
     float mb = Mr;
 #pragma unroll
-    for (int j = 0; j < BATCH; ++j)
-      if (j0 + j < nj) mb = fmax_nc(mb, u32_as_f32(mv[j].x));
+    for (int j = 0; j < BATCH; ++j) {
+      mj[j] = j0 + j < nj ? u32_as_f32(mv[j].x) : kNeg;
+      mb = fmax_nc(mb, mj[j]);
+    }
     const float al = __builtin_amdgcn_exp2f(Mr - mb);
     Lr *= al;
     Or.x *= al; Or.y *= al; Or.z *= al; Or.w *= al;
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
-      if (j0 + j < nj) {
-        const float f = __builtin_amdgcn_exp2f(u32_as_f32(mv[j].x) - mb);
-        Lr = fmaf(u32_as_f32(mv[j].y), f, Lr);
-        Or.x = fmaf(u32_as_f32(ov[j].x), f, Or.x);
-        Or.y = fmaf(u32_as_f32(ov[j].y), f, Or.y);
-        Or.z = fmaf(u32_as_f32(ov[j].z), f, Or.z);
-        Or.w = fmaf(u32_as_f32(ov[j].w), f, Or.w);
-      }
+      const float f = __builtin_amdgcn_exp2f(mj[j] - mb);
+      Lr = fmaf(u32_as_f32(mv[j].y), f, Lr);
+      Or.x = fmaf(u32_as_f32(ov[j].x), f, Or.x);
+      Or.y = fmaf(u32_as_f32(ov[j].y), f, Or.y);
+      Or.z = fmaf(u32_as_f32(ov[j].z), f, Or.z);
+      Or.w = fmaf(u32_as_f32(ov[j].w), f, Or.w);
     }
     Mr = mb;
   }
@@ -918,7 +923,12 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       if (refill) load_k(i, base + NW * CH);
 
       // ---- tile max, rescale of the running state (not for a wave's
-      //      first tile: its accumulators are still zero) ----
+      //      first tile: its accumulators are still zero). The running max
+      //      is a reference, not the exact maximum: it moves (and the state
+      //      is rescaled) only when a row's tile max exceeds it by more than
+      //      kLazyMax, so after the first tiles almost no tile pays for the
+      //      rescale; p = 2^(s - m) then stays below 2^kLazyMax, which fp32
+      //      sums and the bf16 weights hold with their full precision. ----
       {
         float mt[RS][4];
 #pragma unroll
@@ -933,7 +943,7 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
 #pragma unroll
           for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) grow = grow || (mt[rs][r] > m_run[rs][r]);
+            for (int r = 0; r < 4; ++r) grow = grow || (mt[rs][r] > m_run[rs][r] + kLazyMax);
           if (grow) {
 #pragma unroll
             for (int rs = 0; rs < RS; ++rs) {
