@@ -184,6 +184,37 @@ def test_gpt2_random_init_decode_matches_reference():
     assert cq.get_seq_length(0) == 26
 
 
+def test_gpt2_eager_reorder_and_upcast_path():
+    """GPT-2 with reorder_and_upcast_attn under eager attention: the quantized
+    module attends over the dequantized cache through the model's own
+    _upcast_and_reordered_attn (transformers 5.x signature: query, key, value,
+    attention_mask; reference models/gpt2/gpt2_quant.py:104-106 passes the
+    4.x arguments). Stock eager model with a DynamicCache as the reference, fp32."""
+    cfg = GPT2Config(n_layer=2, n_head=4, n_embd=128, vocab_size=256, n_positions=256,
+                     reorder_and_upcast_attn=True)
+    torch.manual_seed(1)
+    ref = GPT2LMHeadModel(cfg).eval()
+    quant = GPT2LMHeadModel(cfg).eval()
+    quant.load_state_dict(ref.state_dict())
+    ref.set_attn_implementation("eager")
+    quant.set_attn_implementation("eager")
+    replace_gpt2_attention_with_quantized(quant)
+    ref, quant = ref.to(DEV), quant.to(DEV)
+    torch.manual_seed(8)
+    prompt = torch.randint(0, 256, (1, 20), device=DEV)
+    with torch.no_grad():
+        cr, cq = DynamicCache(), GPT2Cache()
+        lr = ref(input_ids=prompt, past_key_values=cr, use_cache=True).logits[:, -1]
+        lq = quant(input_ids=prompt, past_key_values=cq, use_cache=True).logits[:, -1]
+        assert (lr - lq).abs().max().item() < 1.0 and lr.argmax().item() == lq.argmax().item()
+        for _ in range(4):
+            nid = torch.randint(0, 256, (1, 1), device=DEV)
+            lr = ref(input_ids=nid, past_key_values=cr, use_cache=True).logits[:, -1]
+            lq = quant(input_ids=nid, past_key_values=cq, use_cache=True).logits[:, -1]
+            assert (lr - lq).abs().max().item() < 2.0
+    assert cq.get_seq_length(0) == 24
+
+
 def test_cache_append_and_attend_matches_append_then_attend():
     """QuantizedKVCache.append_and_attend (one launch) leaves the same cache
     as append and gives the attention over it, for a uniform and a ragged layer."""
