@@ -81,6 +81,9 @@ def main() -> int:
     ap.add_argument("--unfused", action="store_true",
                     help="three launches per layer (quantize K, quantize V, attention) instead of the "
                          "fused decode step")
+    ap.add_argument("--paged", type=int, default=0, metavar="PAGE_SIZE",
+                    help="keep each layer's cache in a block pool of PAGE_SIZE-row pages (>= 64, a power of "
+                         "two) addressed through a block table, pages in a seeded random order; 0 = contiguous")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -134,16 +137,33 @@ def main() -> int:
     if w["ragged"]:
         lens = torch.randint(128, ctx + 1, (B,), generator=torch.Generator().manual_seed(4))
         seq_lens = lens.to(dev, torch.int32)
+    P = args.paged
+    pt = None
+    if P:
+        if P < 64 or P & (P - 1):
+            print("bench.py: --paged needs a power of two >= 64", file=sys.stderr)
+            return 2
+        pages = -(-S_cap // P)
+        n_blocks = B * pages
+        perm = torch.randperm(n_blocks, generator=torch.Generator().manual_seed(5)).to(torch.int32)
+        pt = ops.PageTable(perm.view(B, pages).contiguous().to(dev), P, n_blocks)
     layers = []
     with torch.cuda.stream(stream):
         for _ in range(L):
-            kp = torch.empty(B, Hkv, S_cap, W_, dtype=torch.uint8, device=dev)
+            if P:
+                kp = torch.empty(Hkv, pt.num_blocks * P, W_, dtype=torch.uint8, device=dev)
+                ks = torch.empty(Hkv, pt.num_blocks * P, NG, dtype=sdt, device=dev)
+            else:
+                kp = torch.empty(B, Hkv, S_cap, W_, dtype=torch.uint8, device=dev)
+                ks = torch.empty(B, Hkv, S_cap, NG, dtype=sdt, device=dev)
             vp = torch.empty_like(kp)
-            ks = torch.empty(B, Hkv, S_cap, NG, dtype=sdt, device=dev)
             vs = torch.empty_like(ks)
             for packed, scales in ((kp, ks), (vp, vs)):
                 x = torch.randn(B, Hkv, ctx, D, generator=gen, device=dev, dtype=torch.float32).to(tdt)
-                ops.quantize_into(x, packed, scales, G, 0)
+                if P:
+                    ops.quantize_into_paged(x, packed, scales, pt, G, 0)
+                else:
+                    ops.quantize_into(x, packed, scales, G, 0)
                 del x
             layer = dict(
                 kp=kp, ks=ks, vp=vp, vs=vs,
@@ -169,6 +189,19 @@ def main() -> int:
     fused = not args.unfused and w["dtype"] != "f32" and G in (32, 64, 128)
 
     def attn(layer):
+        if P:
+            if fused:
+                ops.decode_step_paged(
+                    layer["q"], layer["knew"], layer["vnew"], layer["kp"], layer["ks"], layer["vp"], layer["vs"],
+                    pt, pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm_scale, out=layer["out"],
+                )
+            else:
+                ops.fused_decode_attention_paged(
+                    layer["q"], layer["kp"], layer["ks"], layer["vp"], layer["vs"], pt,
+                    n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm_scale,
+                    seq_lens=seq_plus, seq_len=None if seq_plus is not None else attended, out=layer["out"],
+                )
+            return
         if fused:
             ops.decode_step(
                 layer["q"], layer["knew"], layer["vnew"], layer["kp"], layer["ks"], layer["vp"], layer["vs"],
@@ -184,7 +217,10 @@ def main() -> int:
 
     def step():
         for layer in layers:
-            if not fused:
+            if not fused and P:
+                ops.quantize_into_paged(layer["knew"], layer["kp"], layer["ks"], pt, G, pos)
+                ops.quantize_into_paged(layer["vnew"], layer["vp"], layer["vs"], pt, G, pos)
+            elif not fused:
                 ops.quantize_into(layer["knew"], layer["kp"], layer["ks"], G, pos)
                 ops.quantize_into(layer["vnew"], layer["vp"], layer["vs"], G, pos)
             attn(layer)
@@ -292,7 +328,7 @@ def main() -> int:
         "config": {
             "workload": w["desc"], "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
             "group_size": G, "context": ctx, "layers": L, "ragged": w["ragged"],
-            "graph": graph is not None, "fused_step": fused,
+            "graph": graph is not None, "fused_step": fused, "paged": P or None,
         },
         "ms_per_token": round(ms_per_step, 5),
         "attn_us_per_layer": round(attn_us, 3),

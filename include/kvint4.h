@@ -194,6 +194,83 @@ int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
                     int64_t n_split, void* workspace, int64_t workspace_bytes,
                     void* stream);
 
+/*
+ * Paged caches.
+ *
+ * The reference keeps one contiguous tensor per layer and grows it with
+ * torch.cat (models/llama3/kv_cache.py:76-105); it has no paged layout. These
+ * entry points are the paged counterparts of the ones above (same arguments
+ * and semantics) for a cache whose rows live in a block pool:
+ *
+ *   pools:  codes [H, num_blocks * page_size, W] uint8 and scales
+ *           [H, num_blocks * page_size, num_groups] of scale_dtype; the stride
+ *           arrays are [2]: (head, row), bytes for codes, elements for scales.
+ *   block_table: device int32 [B, table_stride]; token t of sequence b is pool
+ *           row block_table[b * table_stride + t / page_size] * page_size +
+ *           t % page_size, for t < table_cols * page_size. page_size is a power
+ *           of two. An entry < 0 or >= num_blocks marks a page with no block:
+ *           writes to it are dropped and its rows are absent (dequantize writes
+ *           zeros; attention never reads past a sequence's length, and its
+ *           length must not reach such a page).
+ *
+ * The attention entry points (kvq_decode_attn_paged, kvq_decode_step_paged)
+ * need bf16/fp16 queries, 16-bit scales and page_size >= 64; a head's pool
+ * must stay below 2 GiB. Planning and workspace: kvq_decode_attn_num_splits
+ * (s_max = the longest attended length) and kvq_decode_attn_workspace_bytes,
+ * as for the contiguous cache.
+ */
+int kvq_quantize_paged(const void* x, int x_dtype, const int64_t* x_strides,
+                       int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
+                       void* packed_pool, const int64_t* pool_strides,
+                       void* scale_pool, int scale_dtype, const int64_t* scale_pool_strides,
+                       const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+                       int64_t num_blocks, int64_t page_size,
+                       const int32_t* write_pos, int64_t write_pos0,
+                       void* stream);
+
+int kvq_dequantize_paged(const void* packed_pool, const int64_t* pool_strides,
+                         const void* scale_pool, int scale_dtype, const int64_t* scale_pool_strides,
+                         const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+                         int64_t num_blocks, int64_t page_size,
+                         int64_t B, int64_t H, int64_t S, int64_t group_size, int64_t num_groups,
+                         void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
+                         void* stream);
+
+/* Keys of sequence b: its first seq_lens[b] tokens (seq_lens: device int32
+ * [B]), or seq_len for every sequence when seq_lens is NULL. */
+int kvq_decode_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,
+                          const void* k_pool, const int64_t* kp_strides,
+                          const void* k_scale_pool, const int64_t* ks_strides,
+                          const void* v_pool, const int64_t* vp_strides,
+                          const void* v_scale_pool, const int64_t* vs_strides,
+                          int scale_dtype,
+                          const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+                          int64_t num_blocks, int64_t page_size,
+                          void* out, const int64_t* out_strides,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                          int64_t group_size, const int32_t* seq_lens, int64_t seq_len,
+                          int is_causal, float sm_scale,
+                          int64_t n_split, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* Capacity = table_cols * page_size; a position whose page has no block is
+ * neither written nor attended. */
+int kvq_decode_step_paged(const void* q, int q_dtype, const int64_t* q_strides,
+                          const void* k_new, const int64_t* kn_strides,
+                          const void* v_new, const int64_t* vn_strides,
+                          void* k_pool, const int64_t* kp_strides,
+                          void* k_scale_pool, const int64_t* ks_strides,
+                          void* v_pool, const int64_t* vp_strides,
+                          void* v_scale_pool, const int64_t* vs_strides,
+                          int scale_dtype,
+                          const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+                          int64_t num_blocks, int64_t page_size,
+                          void* out, const int64_t* out_strides,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t group_size,
+                          const int32_t* positions, int64_t pos0, float sm_scale,
+                          int64_t n_split, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

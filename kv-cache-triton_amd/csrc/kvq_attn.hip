@@ -74,6 +74,15 @@ struct AttnArgs {
   const void* knew;
   const void* vnew;
   int64_t kns_b, kns_h, vns_b, vns_h;
+  // paged cache (kernels instantiated with PAGED): kp/ks/vp/vs are pools
+  // [Hkv, n_blocks << page_shift, ...] (batch strides 0, row strides k*s_s),
+  // sequence b's token t is pool row bt[b * bt_stride + (t >> page_shift)]
+  // << page_shift | (t & (page size - 1)); entries outside [0, n_blocks), or
+  // pages >= bt_cols, have no rows. pool_rows = n_blocks << page_shift.
+  const int32_t* bt;
+  int64_t bt_stride;
+  int bt_cols, n_blocks, page_shift;
+  uint32_t pool_rows;
   uint32_t* ws_cnt;  // [kCntUnits][kSubCnt + 1] arrival counters, kCntStride
                      // words apart (zero between calls)
   float* ws_ml;      // [n_units][n_split][ROWS][2]  (max, sum)
@@ -206,6 +215,25 @@ __device__ __forceinline__ void split_range(const AttnArgs& a, int L, int split,
   const uint32_t ns = (uint32_t)a.n_split;
   t0 = (int)(((uint32_t)split * (uint32_t)L) / ns);
   t1 = (int)(((uint32_t)(split + 1) * (uint32_t)L) / ns);
+}
+
+// The same with split boundaries rounded down to multiples of 64 keys, so
+// that every 64-key tile of a split lies inside one page of a paged cache
+// (pages are multiples of 64 rows).
+__device__ __forceinline__ void split_range64(const AttnArgs& a, int L, int split, int& t0, int& t1) {
+  const uint32_t ns = (uint32_t)a.n_split;
+  t0 = split == 0 ? 0 : (int)((((uint32_t)split * (uint32_t)L) / ns) & ~63u);
+  t1 = split + 1 == (int)ns ? L : (int)((((uint32_t)(split + 1) * (uint32_t)L) / ns) & ~63u);
+}
+
+// Pool row offset of token t of a paged sequence (bt_b = its block table
+// row), relative to t: row = t + delta. ok is false when no block holds t.
+__device__ __forceinline__ void page_delta(const AttnArgs& a, const int32_t* bt_b, uint32_t t,
+                                           uint32_t& delta, bool& ok) {
+  const uint32_t pg = t >> a.page_shift;
+  const int32_t blk = pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1;
+  ok = blk >= 0 && blk < a.n_blocks;
+  delta = ((uint32_t)blk - pg) << a.page_shift;
 }
 
 constexpr int kMaxRows = 8;  // query rows per workgroup (both kernels)
@@ -502,7 +530,7 @@ __device__ __forceinline__ void chunk_scales(uint2 raw, bool g32, const uint32_t
   }
 }
 
-template <int D, int RS, int QM, int SM, bool ROWMASK, int NW, int CH>
+template <int D, int RS, int QM, int SM, bool ROWMASK, int NW, int CH, bool PAGED>
 __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArgs a) {
   constexpr bool F16 = QM == KVQ_F16;
   constexpr bool S_F16 = SM == KVQ_F16;
@@ -553,10 +581,24 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   L = L < 0 ? 0 : L;
   // decode step: the new token goes to row L (if it fits the cache) and is
   // attended by the unit's last split from registers
-  const bool has_new = a.append && L < a.Sk && split == a.n_split - 1;
+  bool has_new = a.append && L < a.Sk && split == a.n_split - 1;
   L = L < a.Sk ? L : a.Sk;
   int t_begin, t_end;
-  split_range(a, L, split, t_begin, t_end);
+  if constexpr (PAGED) split_range64(a, L, split, t_begin, t_end);
+  else split_range(a, L, split, t_begin, t_end);
+  const int32_t* bt_b = PAGED ? a.bt + (int64_t)b * a.bt_stride : nullptr;
+  // decode step: the cache row the new token goes to (paged: its pool row; a
+  // position no block holds is neither written nor attended)
+  int64_t new_row = L;
+  if constexpr (PAGED) {
+    if (has_new) {
+      uint32_t dl;
+      bool ok;
+      page_delta(a, bt_b, (uint32_t)L, dl, ok);
+      has_new = ok;
+      new_row = (int64_t)(uint32_t)((uint32_t)L + dl);
+    }
+  }
   // Tiles of 64 keys, dealt to the waves round-robin. A split of whole passes
   // (NW tiles each) plus at most NW keys does not open another pass for those
   // few keys (it would cost one wave a whole tile): wave w folds tail key w
@@ -571,19 +613,51 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
     }
   }
 
-  // ---- cache slices as bounds-checked buffers (rows >= L read as zero) ----
+  // ---- cache slices as bounds-checked buffers (contiguous: rows >= t_end
+  //      read as zero; paged: the KV head's pool, rows addressed through the
+  //      block table, tokens >= t_end given an out-of-range offset) ----
   const uint8_t* kp_bh = a.kp + (int64_t)b * a.kps_b + (int64_t)kvh * a.kps_h;
   const uint8_t* vp_bh = a.vp + (int64_t)b * a.vps_b + (int64_t)kvh * a.vps_h;
   const uint16_t* ks_bh = (const uint16_t*)a.ks + ((int64_t)b * a.kss_b + (int64_t)kvh * a.kss_h);
   const uint16_t* vs_bh = (const uint16_t*)a.vs + ((int64_t)b * a.vss_b + (int64_t)kvh * a.vss_h);
   const uint32_t kps = (uint32_t)a.kps_s, vps = (uint32_t)a.vps_s;
   const uint32_t kss2 = 2u * (uint32_t)a.kss_s, vss2 = 2u * (uint32_t)a.vss_s;
-  // Rows at or past this split's end read as zero and move no bytes.
-  const uint32_t Le = (uint32_t)t_end;
+  const uint32_t Le = PAGED ? a.pool_rows : (uint32_t)t_end;
   const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kp_bh, Le * kps);
   const __amdgpu_buffer_rsrc_t rks = buffer_rsrc(ks_bh, Le * kss2);
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vp_bh, Le * vps);
   const __amdgpu_buffer_rsrc_t rvs = buffer_rsrc(vs_bh, Le * vss2);
+  // Paged tiles: a 64-key tile starting at t0 (a multiple of 64) lies in one
+  // page, so its keys are rows t0 + delta + j for j < lim (lim = the keys it
+  // has before t_end, 0 if no block holds the page); key j >= lim is given the
+  // pool's end as offset and reads zero.
+  // The block of each of this wave's tiles (tiles wave, wave + NW, ... of
+  // the split; lane k holds tile k's), read from the table once here so that
+  // a refill's loads wait for no table read. The first CH tiles (loaded at
+  // once, before this read could return) and tiles past the 64th read the
+  // table directly.
+  int32_t wave_blk = -1;
+  if constexpr (PAGED) {
+    const int tk = wave + NW * lane;
+    if (tk < ntiles) {
+      const uint32_t pg = ((uint32_t)t_begin + 64u * (uint32_t)tk) >> a.page_shift;
+      wave_blk = pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1;
+    }
+  }
+  auto tile_rows = [&](uint32_t t0, uint32_t& rb, uint32_t& lim) {
+    rb = t0;
+    lim = 64;
+    if constexpr (PAGED) {
+      const uint32_t pg = t0 >> a.page_shift;
+      const uint32_t k = (((t0 - (uint32_t)t_begin) >> 6) - (uint32_t)wave) / (uint32_t)NW;  // wave-uniform
+      int32_t blk;
+      if (k >= (uint32_t)CH && k < 64u) blk = __builtin_amdgcn_readlane(wave_blk, (int)k);
+      else blk = pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1;
+      const bool ok = blk >= 0 && blk < a.n_blocks;
+      rb = t0 + (((uint32_t)blk - pg) << a.page_shift);
+      lim = (ok && t0 < (uint32_t)t_end) ? min(64u, (uint32_t)t_end - t0) : 0u;
+    }
+  };
   const int ng = (D + a.G - 1) / a.G;  // scales per token row: 1, 2 or 4 (wave-uniform)
   const bool g32 = a.G == 32;
   uint32_t gsh[LPT];  // bit offset of each 32-dim chunk's scale in the loaded scale row
@@ -615,21 +689,28 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   };
   auto tile_t0 = [&](int i, int base) { return (uint32_t)(t_begin + (base + NW * i) * 64); };
   auto load_k = [&](int i, int base) {
-    const uint32_t t = tile_t0(i, base) + lane;
+    uint32_t rb, lim;
+    tile_rows(tile_t0(i, base), rb, lim);
+    const uint32_t r = rb + lane;
+    const bool in = !PAGED || (uint32_t)lane < lim;
 #pragma unroll
     for (int c = 0; c < LPT; ++c)
-      kc4[i][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, t * kps + 16u * c, 0, 0));
-    skr[i] = load_scales(rks, t * kss2);
+      kc4[i][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rk, in ? r * kps + 16u * c : Le * kps, 0, 0));
+    skr[i] = load_scales(rks, in ? r * kss2 : Le * kss2);
   };
   auto load_v = [&](int i, int base) {
-    const uint32_t t0 = tile_t0(i, base);
-    svr[i] = load_scales(rvs, (t0 + lane) * vss2);
+    uint32_t rb, lim;
+    tile_rows(tile_t0(i, base), rb, lim);
+    svr[i] = load_scales(rvs, (!PAGED || (uint32_t)lane < lim) ? (rb + lane) * vss2 : Le * vss2);
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t j = (uint32_t)(s * SUB + VTS * k + vts);
         vq[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(
-            rv, (t0 + (uint32_t)(s * SUB + VTS * k + vts)) * vps + 4u * (uint32_t)vj, 0, 0);
+            rv, (!PAGED || j < lim) ? (rb + j) * vps + 4u * (uint32_t)vj : Le * vps, 0, 0);
+      }
   };
 
   // ---- loads: the query rows first (wave-private copy: QT pieces of 8
@@ -685,7 +766,14 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const int tail_t = t_begin + 64 * ntiles + wave;
   uint32_t tail_kb = 0u, tail_vb = 0u, tail_ks = 0u, tail_vs = 0u;
   if (wave < n_tail) {
-    const uint32_t tt = (uint32_t)tail_t, col = (uint32_t)(lane % (D / 2));
+    uint32_t tt = (uint32_t)tail_t;
+    const uint32_t col = (uint32_t)(lane % (D / 2));
+    if constexpr (PAGED) {
+      uint32_t dl;
+      bool ok;
+      page_delta(a, bt_b, tt, dl, ok);
+      tt = ok ? tt + dl : Le;  // no block: the pool's end, reads zero
+    }
     const uint32_t sg = 2u * (uint32_t)((2 * (lane % (D / 2))) / a.G);
     tail_kb = __builtin_amdgcn_raw_buffer_load_b8(rk, tt * kps + col, 0, 0);
     tail_vb = __builtin_amdgcn_raw_buffer_load_b8(rv, tt * vps + col, 0, 0);
@@ -833,8 +921,8 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       c1 = fminf(fmaxf(c1, -8.0f), 7.0f);
       const uint32_t byte = (uint32_t)((int)c0 + 8) | ((uint32_t)((int)c1 + 8) << 4);
       const uint32_t sbits = S_F16 ? f32_to_f16_bits(scale) : f32_to_bf16_bits(scale);
-      uint8_t* prow = const_cast<uint8_t*>(kvsel == 0 ? kp_bh : vp_bh) + (int64_t)L * (kvsel == 0 ? kps : vps);
-      uint16_t* srow = const_cast<uint16_t*>(kvsel == 0 ? ks_bh : vs_bh) + (int64_t)L * (kvsel == 0 ? a.kss_s : a.vss_s);
+      uint8_t* prow = const_cast<uint8_t*>(kvsel == 0 ? kp_bh : vp_bh) + new_row * (kvsel == 0 ? kps : vps);
+      uint16_t* srow = const_cast<uint16_t*>(kvsel == 0 ? ks_bh : vs_bh) + new_row * (kvsel == 0 ? a.kss_s : a.vss_s);
       if (byte_ok) prow[lane] = (uint8_t)byte;
       if (byte_ok && (2 * lane) % G == 0) srow[(2 * lane) / G] = (uint16_t)sbits;
       const float sq = scale16_to_f32(sbits, S_F16);
@@ -1457,23 +1545,29 @@ template <int RS>
 constexpr int mfma_waves() { return RS == 1 ? 8 : 4; }
 constexpr int kMfmaTilesInFlight = 2;
 
-template <int D, int RS, int QM, int SM>
+template <int D, int RS, int QM, int SM, bool PAGED>
 static void launch_mfma_rs(const AttnArgs& a, bool rowmask, dim3 grid, hipStream_t st) {
   constexpr int NW = mfma_waves<RS>();
   constexpr int CH = kMfmaTilesInFlight;
-  if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, true, NW, CH>), grid, dim3(64 * NW), 0, st, a);
-  else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, false, NW, CH>), grid, dim3(64 * NW), 0, st, a);
+  if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, true, NW, CH, PAGED>), grid, dim3(64 * NW), 0, st, a);
+  else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, false, NW, CH, PAGED>), grid, dim3(64 * NW), 0, st, a);
+}
+
+template <int D, int QM, bool PAGED>
+static void launch_mfma_pg(const AttnArgs& a, int rows, bool rowmask, dim3 grid, hipStream_t st) {
+  if (a.scale_dtype == KVQ_F16) {
+    if (rows <= 4) launch_mfma_rs<D, 1, QM, KVQ_F16, PAGED>(a, rowmask, grid, st);
+    else launch_mfma_rs<D, 2, QM, KVQ_F16, PAGED>(a, rowmask, grid, st);
+  } else {
+    if (rows <= 4) launch_mfma_rs<D, 1, QM, KVQ_BF16, PAGED>(a, rowmask, grid, st);
+    else launch_mfma_rs<D, 2, QM, KVQ_BF16, PAGED>(a, rowmask, grid, st);
+  }
 }
 
 template <int D, int QM>
 static void launch_mfma(const AttnArgs& a, int rows, bool rowmask, dim3 grid, hipStream_t st) {
-  if (a.scale_dtype == KVQ_F16) {
-    if (rows <= 4) launch_mfma_rs<D, 1, QM, KVQ_F16>(a, rowmask, grid, st);
-    else launch_mfma_rs<D, 2, QM, KVQ_F16>(a, rowmask, grid, st);
-  } else {
-    if (rows <= 4) launch_mfma_rs<D, 1, QM, KVQ_BF16>(a, rowmask, grid, st);
-    else launch_mfma_rs<D, 2, QM, KVQ_BF16>(a, rowmask, grid, st);
-  }
+  if (a.bt) launch_mfma_pg<D, QM, true>(a, rows, rowmask, grid, st);
+  else launch_mfma_pg<D, QM, false>(a, rows, rowmask, grid, st);
 }
 
 template <int D, int ROWS, int QM>
@@ -1562,6 +1656,13 @@ struct StepArgs {
   int64_t pos0;
 };
 
+// Paged-cache extras: the block table and the pools' geometry. The stride
+// arrays passed along with them are (0, head, row): pools have no batch axis.
+struct PagedArgs {
+  const int32_t* bt;
+  int64_t bt_stride, bt_cols, n_blocks, page_size;
+};
+
 static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides,
                                const void* k_packed, const int64_t* kp_strides,
                                const void* k_scales, const int64_t* ks_strides,
@@ -1573,7 +1674,7 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
                                int64_t group_size, int64_t Sk,
                                const int32_t* seq_lens, int is_causal, float sm_scale,
                                int64_t n_split, void* workspace, int64_t workspace_bytes,
-                               void* stream, const StepArgs* step) {
+                               void* stream, const StepArgs* step, const PagedArgs* pg) {
   KVQ_CHECK_ARG(dtype_ok(q_dtype), "kvq_decode_attn: q dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_decode_attn: scale dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(q_strides && kp_strides && ks_strides && vp_strides && vs_strides && out_strides,
@@ -1618,11 +1719,26 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
       return KVQ_EUNSUP;
     }
   }
-  // Token offsets inside one (batch, head) slice are 32-bit.
-  if (Sk > 0 && (Sk * kp_strides[2] >= (1ll << 31) || Sk * vp_strides[2] >= (1ll << 31) ||
-                 Sk * ks_strides[2] * 4 >= (1ll << 31) || Sk * vs_strides[2] * 4 >= (1ll << 31))) {
-    set_error("kvq_decode_attn: a (batch, head) slice of the cache exceeds 2 GiB");
+  // Token offsets inside one (batch, head) slice, or one head's pool, are 32-bit.
+  const int64_t rows_addr = pg ? pg->n_blocks * pg->page_size : Sk;
+  if (rows_addr > 0 && (rows_addr * kp_strides[2] >= (1ll << 31) || rows_addr * vp_strides[2] >= (1ll << 31) ||
+                        rows_addr * ks_strides[2] * 4 >= (1ll << 31) || rows_addr * vs_strides[2] * 4 >= (1ll << 31))) {
+    set_error("kvq_decode_attn: a (batch, head) slice of the cache (or a head's pool) exceeds 2 GiB");
     return KVQ_EUNSUP;
+  }
+  if (pg) {
+    KVQ_CHECK_ARG(pg->page_size >= 64 && (pg->page_size & (pg->page_size - 1)) == 0 && pg->page_size <= (1 << 20),
+                  "kvq_decode_attn_paged: page_size must be a power of two >= 64 (got %lld)",
+                  (long long)pg->page_size);
+    KVQ_CHECK_ARG(pg->n_blocks >= 0 && pg->n_blocks < (1ll << 31) && pg->bt_cols >= 0 &&
+                      pg->bt_cols < (1ll << 31) && pg->bt_stride >= pg->bt_cols,
+                  "kvq_decode_attn_paged: bad block table geometry");
+    KVQ_CHECK_ARG(pg->bt != nullptr || pg->bt_cols == 0, "kvq_decode_attn_paged: null block table");
+    if (!mfma) {
+      set_error("kvq_decode_attn_paged: paged caches take the matrix-core kernel (bf16/fp16 queries, "
+                "16-bit scales)");
+      return KVQ_EUNSUP;
+    }
   }
   KVQ_CHECK_ARG(Sk * kMaxSplit < (1ll << 32) && Sq <= 0x7fffffffll, "kvq_decode_attn: sequence too long");
 
@@ -1672,6 +1788,14 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
   a.vnew = step ? step->vnew : nullptr;
   a.kns_b = step ? step->kn_strides[0] : 0; a.kns_h = step ? step->kn_strides[1] : 0;
   a.vns_b = step ? step->vn_strides[0] : 0; a.vns_h = step ? step->vn_strides[1] : 0;
+  a.bt = pg ? pg->bt : nullptr;
+  a.bt_stride = pg ? pg->bt_stride : 0;
+  a.bt_cols = pg ? (int)pg->bt_cols : 0;
+  a.n_blocks = pg ? (int)pg->n_blocks : 0;
+  a.page_shift = 0;
+  if (pg)
+    while ((int64_t(1) << a.page_shift) < pg->page_size) ++a.page_shift;
+  a.pool_rows = pg ? (uint32_t)(pg->n_blocks * pg->page_size) : 0u;
   a.ws_cnt = nullptr; a.ws_ml = nullptr; a.ws_o = nullptr;
   if (need > 0) {
     char* w = (char*)workspace;
@@ -1704,24 +1828,23 @@ extern "C" int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_stri
   return decode_attn_impl(q, q_dtype, q_strides, k_packed, kp_strides, k_scales, ks_strides, v_packed,
                           vp_strides, v_scales, vs_strides, scale_dtype, out, out_strides, B, Hq, Hkv, Sq,
                           D, group_size, Sk, seq_lens, is_causal, sm_scale, n_split, workspace,
-                          workspace_bytes, stream, nullptr);
+                          workspace_bytes, stream, nullptr, nullptr);
 }
 
-extern "C" int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
-                               const void* k_new, const int64_t* kn_strides,
-                               const void* v_new, const int64_t* vn_strides,
-                               void* k_packed, const int64_t* kp_strides,
-                               void* k_scales, const int64_t* ks_strides,
-                               void* v_packed, const int64_t* vp_strides,
-                               void* v_scales, const int64_t* vs_strides,
-                               int scale_dtype,
-                               void* out, const int64_t* out_strides,
-                               int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
-                               int64_t group_size, int64_t capacity,
-                               const int32_t* positions, int64_t pos0, float sm_scale,
-                               int64_t n_split, void* workspace, int64_t workspace_bytes,
-                               void* stream) {
-  clear_error();
+static int decode_step_impl(const void* q, int q_dtype, const int64_t* q_strides,
+                            const void* k_new, const int64_t* kn_strides,
+                            const void* v_new, const int64_t* vn_strides,
+                            void* k_packed, const int64_t* kp_strides,
+                            void* k_scales, const int64_t* ks_strides,
+                            void* v_packed, const int64_t* vp_strides,
+                            void* v_scales, const int64_t* vs_strides,
+                            int scale_dtype,
+                            void* out, const int64_t* out_strides,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                            int64_t group_size, int64_t capacity,
+                            const int32_t* positions, int64_t pos0, float sm_scale,
+                            int64_t n_split, void* workspace, int64_t workspace_bytes,
+                            void* stream, const PagedArgs* pg) {
   KVQ_CHECK_ARG(dtype_ok(q_dtype) && dtype_ok(scale_dtype), "kvq_decode_step: bad dtype");
   KVQ_CHECK_ARG(kn_strides && vn_strides && q_strides, "kvq_decode_step: null stride array");
   if (!use_mfma(q_dtype, scale_dtype) || !(group_size == 32 || group_size == 64 || group_size == 128)) {
@@ -1746,5 +1869,91 @@ extern "C" int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_stri
   return decode_attn_impl(q, q_dtype, q_strides, k_packed, kp_strides, k_scales, ks_strides, v_packed,
                           vp_strides, v_scales, vs_strides, scale_dtype, out, out_strides, B, Hq, Hkv, 1,
                           D, group_size, capacity, positions, 0, sm_scale, n_split, workspace,
-                          workspace_bytes, stream, &step);
+                          workspace_bytes, stream, &step, pg);
+}
+
+extern "C" int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
+                               const void* k_new, const int64_t* kn_strides,
+                               const void* v_new, const int64_t* vn_strides,
+                               void* k_packed, const int64_t* kp_strides,
+                               void* k_scales, const int64_t* ks_strides,
+                               void* v_packed, const int64_t* vp_strides,
+                               void* v_scales, const int64_t* vs_strides,
+                               int scale_dtype,
+                               void* out, const int64_t* out_strides,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                               int64_t group_size, int64_t capacity,
+                               const int32_t* positions, int64_t pos0, float sm_scale,
+                               int64_t n_split, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  clear_error();
+  return decode_step_impl(q, q_dtype, q_strides, k_new, kn_strides, v_new, vn_strides, k_packed,
+                          kp_strides, k_scales, ks_strides, v_packed, vp_strides, v_scales, vs_strides,
+                          scale_dtype, out, out_strides, B, Hq, Hkv, D, group_size, capacity, positions,
+                          pos0, sm_scale, n_split, workspace, workspace_bytes, stream, nullptr);
+}
+
+namespace {
+// (head, row) pool strides -> the (batch, head, row) arrays of the contiguous
+// code path, with batch stride 0.
+struct Strides3 {
+  int64_t v[3];
+  Strides3(const int64_t* hr) : v{0, hr ? hr[0] : 0, hr ? hr[1] : 0} {}
+};
+}  // namespace
+
+extern "C" int kvq_decode_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,
+                                     const void* k_pool, const int64_t* kp_strides,
+                                     const void* k_scale_pool, const int64_t* ks_strides,
+                                     const void* v_pool, const int64_t* vp_strides,
+                                     const void* v_scale_pool, const int64_t* vs_strides,
+                                     int scale_dtype,
+                                     const int32_t* block_table, int64_t table_stride,
+                                     int64_t table_cols, int64_t num_blocks, int64_t page_size,
+                                     void* out, const int64_t* out_strides,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                     int64_t group_size, const int32_t* seq_lens, int64_t seq_len,
+                                     int is_causal, float sm_scale,
+                                     int64_t n_split, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(kp_strides && ks_strides && vp_strides && vs_strides, "kvq_decode_attn_paged: null stride array");
+  KVQ_CHECK_ARG(page_size >= 1 && table_cols >= 0 && table_cols <= (1ll << 31) / page_size,
+                "kvq_decode_attn_paged: bad page size or table width");
+  const int64_t cap = table_cols * page_size;
+  KVQ_CHECK_ARG(seq_lens != nullptr || (seq_len >= 0 && seq_len <= cap),
+                "kvq_decode_attn_paged: seq_len %lld outside [0, %lld]", (long long)seq_len, (long long)cap);
+  const PagedArgs pg{block_table, table_stride, table_cols, num_blocks, page_size};
+  const Strides3 kp(kp_strides), ks(ks_strides), vp(vp_strides), vs(vs_strides);
+  return decode_attn_impl(q, q_dtype, q_strides, k_pool, kp.v, k_scale_pool, ks.v, v_pool, vp.v,
+                          v_scale_pool, vs.v, scale_dtype, out, out_strides, B, Hq, Hkv, Sq, D, group_size,
+                          seq_lens ? cap : seq_len, seq_lens, is_causal, sm_scale, n_split, workspace,
+                          workspace_bytes, stream, nullptr, &pg);
+}
+
+extern "C" int kvq_decode_step_paged(const void* q, int q_dtype, const int64_t* q_strides,
+                                     const void* k_new, const int64_t* kn_strides,
+                                     const void* v_new, const int64_t* vn_strides,
+                                     void* k_pool, const int64_t* kp_strides,
+                                     void* k_scale_pool, const int64_t* ks_strides,
+                                     void* v_pool, const int64_t* vp_strides,
+                                     void* v_scale_pool, const int64_t* vs_strides,
+                                     int scale_dtype,
+                                     const int32_t* block_table, int64_t table_stride,
+                                     int64_t table_cols, int64_t num_blocks, int64_t page_size,
+                                     void* out, const int64_t* out_strides,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t group_size,
+                                     const int32_t* positions, int64_t pos0, float sm_scale,
+                                     int64_t n_split, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(kp_strides && ks_strides && vp_strides && vs_strides, "kvq_decode_step_paged: null stride array");
+  KVQ_CHECK_ARG(page_size >= 1 && table_cols >= 1 && table_cols <= (1ll << 31) / page_size,
+                "kvq_decode_step_paged: bad page size or table width");
+  const PagedArgs pg{block_table, table_stride, table_cols, num_blocks, page_size};
+  const Strides3 kp(kp_strides), ks(ks_strides), vp(vp_strides), vs(vs_strides);
+  return decode_step_impl(q, q_dtype, q_strides, k_new, kn_strides, v_new, vn_strides, k_pool, kp.v,
+                          k_scale_pool, ks.v, v_pool, vp.v, v_scale_pool, vs.v, scale_dtype, out,
+                          out_strides, B, Hq, Hkv, D, group_size, table_cols * page_size, positions, pos0,
+                          sm_scale, n_split, workspace, workspace_bytes, stream, &pg);
 }

@@ -43,6 +43,27 @@ __device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float
   else ((float*)p)[i] = v;
 }
 
+// Paged cache rows. A pool holds num_blocks blocks of 2^page_shift rows per
+// head; sequence b's token t lives in pool row
+//   table[b * tab_stride + (t >> page_shift)] << page_shift | (t & (page_size - 1)).
+// table == nullptr means the contiguous [B, H, S] layout. A table entry that
+// is negative or >= n_blocks, or a page index >= n_pages, has no row (-1).
+struct PageMap {
+  const int32_t* table;
+  int64_t tab_stride;  // int32 entries between sequences' table rows
+  int64_t n_pages;     // entries of a table row in use
+  int64_t n_blocks;    // blocks in the pool
+  int page_shift;
+};
+
+__device__ __forceinline__ int64_t page_row(const PageMap& m, int64_t b, int64_t t) {
+  const int64_t p = t >> m.page_shift;
+  if (t < 0 || p >= m.n_pages) return -1;
+  const int64_t blk = m.table[b * m.tab_stride + p];
+  if (blk < 0 || blk >= m.n_blocks) return -1;
+  return (blk << m.page_shift) | (t & ((int64_t(1) << m.page_shift) - 1));
+}
+
 inline int dtype_size(int dt) { return dt == KVQ_F32 ? 4 : 2; }
 inline bool dtype_ok(int dt) { return dt == KVQ_BF16 || dt == KVQ_F16 || dt == KVQ_F32; }
 

@@ -32,7 +32,14 @@ struct QuantArgs {
   const int32_t* write_pos;
   int64_t write_pos0;
   int x_dtype, scale_dtype;
+  PageMap pm;  // pm.table != nullptr: packed/scales are pools (ps_b = ss_b = 0)
 };
+
+// Destination row of (b, position) and whether it exists: the position
+// itself in the contiguous layout, its pool row in the paged one.
+__device__ __forceinline__ int64_t dest_row(const QuantArgs& a, int64_t b, int64_t pos) {
+  return a.pm.table ? page_row(a.pm, b, pos) : pos;
+}
 
 template <int XDT>
 __device__ __forceinline__ float ld_x(const void* p, int64_t i) {
@@ -61,7 +68,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
   // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
   const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
 
-  const int64_t pos = (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s;
+  const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s);
+  if (pos < 0) return;  // paged: no block holds this position
   uint8_t* prow = a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + g * a.bpg;
 
   for (int64_t j = 0; j < a.bpg; ++j) {
@@ -152,7 +160,8 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     qf = fminf(fmaxf(qf, -8.0f), 7.0f);
     word |= (uint32_t)((int)qf + 8) << (4 * e);
   }
-  const int64_t pos = (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s;
+  const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s);
+  if (pos < 0) return;  // paged: no block holds this position
   // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
   *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
   if (ch % LPG == 0) {
@@ -170,6 +179,7 @@ struct DequantArgs {
   void* out;
   int64_t os_b, os_h, os_s, os_d;
   int scale_dtype, out_dtype;
+  PageMap pm;  // pm.table != nullptr: packed/scales are pools (ps_b = ss_b = 0)
 };
 
 __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
@@ -182,9 +192,15 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
   const int64_t h = bh % a.H;
   const int64_t b = bh / a.H;
 
-  const uint8_t* prow = a.packed + b * a.ps_b + h * a.ps_h + s * a.ps_s + g * a.bpg;
-  const float scale = load_as_f32(a.scales, b * a.ss_b + h * a.ss_h + s * a.ss_s + g, a.scale_dtype);
   const int64_t obase = b * a.os_b + h * a.os_h + s * a.os_s;
+  const int64_t r = a.pm.table ? page_row(a.pm, b, s) : s;
+  if (r < 0) {  // paged: no block holds this position -> zeros
+    for (int64_t c = g * a.G; c < (g + 1) * a.G && c < a.d_out; ++c)
+      store_from_f32(a.out, obase + c * a.os_d, a.out_dtype, 0.0f);
+    return;
+  }
+  const uint8_t* prow = a.packed + b * a.ps_b + h * a.ps_h + r * a.ps_s + g * a.bpg;
+  const float scale = load_as_f32(a.scales, b * a.ss_b + h * a.ss_h + r * a.ss_s + g, a.scale_dtype);
   for (int64_t k = 0; k < a.G; ++k) {
     const int64_t c = g * a.G + k;
     if (c >= a.d_out) break;
@@ -199,13 +215,36 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
 
 using namespace kvq;
 
-extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides,
-                            int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
-                            void* packed, const int64_t* packed_strides,
-                            void* scales, int scale_dtype, const int64_t* scale_strides,
-                            const int32_t* write_pos, int64_t write_pos0,
-                            void* stream) {
-  clear_error();
+namespace {
+
+// Checks a paged-pool description shared by the paged entry points and
+// fills `pm`. Pools are [H, num_blocks << page_shift, ...]; the entry point's
+// stride arrays give (head, row) strides and the batch stride is 0.
+int page_map(const char* who, const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+             int64_t num_blocks, int64_t page_size, int64_t B, PageMap* pm) {
+  KVQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && page_size <= (1 << 20),
+                "%s: page_size must be a power of two in [1, 2^20] (got %lld)", who, (long long)page_size);
+  KVQ_CHECK_ARG(num_blocks >= 0 && table_cols >= 0 && table_stride >= table_cols,
+                "%s: bad block table geometry (num_blocks %lld, cols %lld, stride %lld)", who,
+                (long long)num_blocks, (long long)table_cols, (long long)table_stride);
+  KVQ_CHECK_ARG(block_table != nullptr || B == 0 || table_cols == 0, "%s: null block table", who);
+  KVQ_CHECK_ARG(num_blocks <= (int64_t(1) << 31) / page_size, "%s: pool too large", who);
+  int shift = 0;
+  while ((int64_t(1) << shift) < page_size) ++shift;
+  pm->table = block_table;
+  pm->tab_stride = table_stride;
+  pm->n_pages = table_cols;
+  pm->n_blocks = num_blocks;
+  pm->page_shift = shift;
+  return KVQ_OK;
+}
+
+int quantize_impl(const char* who, const void* x, int x_dtype, const int64_t* x_strides,
+                  int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
+                  void* packed, const int64_t* packed_strides,
+                  void* scales, int scale_dtype, const int64_t* scale_strides,
+                  const int32_t* write_pos, int64_t write_pos0, const PageMap& pm,
+                  void* stream) {
   KVQ_CHECK_ARG(group_size > 0, "kvq_quantize: group_size must be > 0");
   KVQ_CHECK_ARG(dtype_ok(x_dtype), "kvq_quantize: x dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_quantize: scale dtype must be bf16/fp16/fp32");
@@ -230,6 +269,7 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
   a.ss_b = scale_strides[0]; a.ss_h = scale_strides[1]; a.ss_s = scale_strides[2];
   a.write_pos = write_pos; a.write_pos0 = write_pos0;
   a.x_dtype = x_dtype; a.scale_dtype = scale_dtype;
+  a.pm = pm;
 
   hipStream_t st = (hipStream_t)stream;
   const int lpg = (int)(group_size / 8);
@@ -256,7 +296,7 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
       default: KVQ_QVEC(KVQ_F32) break;
     }
 #undef KVQ_QVEC
-    KVQ_CHECK_LAUNCH("kvq_quantize");
+    KVQ_CHECK_LAUNCH(who);
     return KVQ_OK;
   }
 
@@ -268,16 +308,15 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
     case KVQ_F16: hipLaunchKernelGGL(quantize_kernel<KVQ_F16>, grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL(quantize_kernel<KVQ_F32>, grid, block, 0, st, a); break;
   }
-  KVQ_CHECK_LAUNCH("kvq_quantize");
+  KVQ_CHECK_LAUNCH(who);
   return KVQ_OK;
 }
 
-extern "C" int kvq_dequantize(const void* packed, const int64_t* packed_strides,
-                              const void* scales, int scale_dtype, const int64_t* scale_strides,
-                              int64_t B, int64_t H, int64_t S, int64_t group_size, int64_t num_groups,
-                              void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
-                              void* stream) {
-  clear_error();
+int dequantize_impl(const void* packed, const int64_t* packed_strides,
+                    const void* scales, int scale_dtype, const int64_t* scale_strides,
+                    int64_t B, int64_t H, int64_t S, int64_t group_size, int64_t num_groups,
+                    void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
+                    const PageMap& pm, void* stream) {
   KVQ_CHECK_ARG(group_size > 0, "kvq_dequantize: group_size must be > 0");
   KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_dequantize: scale dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(dtype_ok(out_dtype), "kvq_dequantize: out dtype must be bf16/fp16/fp32");
@@ -299,10 +338,77 @@ extern "C" int kvq_dequantize(const void* packed, const int64_t* packed_strides,
   a.out = out;
   a.os_b = out_strides[0]; a.os_h = out_strides[1]; a.os_s = out_strides[2]; a.os_d = out_strides[3];
   a.scale_dtype = scale_dtype; a.out_dtype = out_dtype;
+  a.pm = pm;
 
   const int64_t total = rows * num_groups;
   hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, a);
   KVQ_CHECK_LAUNCH("kvq_dequantize");
   return KVQ_OK;
+}
+
+}  // namespace
+
+extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides,
+                            int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
+                            void* packed, const int64_t* packed_strides,
+                            void* scales, int scale_dtype, const int64_t* scale_strides,
+                            const int32_t* write_pos, int64_t write_pos0,
+                            void* stream) {
+  clear_error();
+  const PageMap pm{nullptr, 0, 0, 0, 0};
+  return quantize_impl("kvq_quantize", x, x_dtype, x_strides, B, H, S, D, group_size, packed,
+                       packed_strides, scales, scale_dtype, scale_strides, write_pos, write_pos0, pm,
+                       stream);
+}
+
+extern "C" int kvq_quantize_paged(const void* x, int x_dtype, const int64_t* x_strides,
+                                  int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
+                                  void* packed_pool, const int64_t* pool_strides,
+                                  void* scale_pool, int scale_dtype, const int64_t* scale_pool_strides,
+                                  const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+                                  int64_t num_blocks, int64_t page_size,
+                                  const int32_t* write_pos, int64_t write_pos0,
+                                  void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(pool_strides && scale_pool_strides, "kvq_quantize_paged: null stride array");
+  PageMap pm;
+  const int rc = page_map("kvq_quantize_paged", block_table, table_stride, table_cols, num_blocks,
+                          page_size, B, &pm);
+  if (rc != KVQ_OK) return rc;
+  const int64_t ps[3] = {0, pool_strides[0], pool_strides[1]};
+  const int64_t ss[3] = {0, scale_pool_strides[0], scale_pool_strides[1]};
+  return quantize_impl("kvq_quantize_paged", x, x_dtype, x_strides, B, H, S, D, group_size,
+                       packed_pool, ps, scale_pool, scale_dtype, ss, write_pos, write_pos0, pm, stream);
+}
+
+extern "C" int kvq_dequantize(const void* packed, const int64_t* packed_strides,
+                              const void* scales, int scale_dtype, const int64_t* scale_strides,
+                              int64_t B, int64_t H, int64_t S, int64_t group_size, int64_t num_groups,
+                              void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
+                              void* stream) {
+  clear_error();
+  const PageMap pm{nullptr, 0, 0, 0, 0};
+  return dequantize_impl(packed, packed_strides, scales, scale_dtype, scale_strides, B, H, S,
+                         group_size, num_groups, out, out_dtype, out_strides, d_out, pm, stream);
+}
+
+extern "C" int kvq_dequantize_paged(const void* packed_pool, const int64_t* pool_strides,
+                                    const void* scale_pool, int scale_dtype,
+                                    const int64_t* scale_pool_strides,
+                                    const int32_t* block_table, int64_t table_stride,
+                                    int64_t table_cols, int64_t num_blocks, int64_t page_size,
+                                    int64_t B, int64_t H, int64_t S, int64_t group_size,
+                                    int64_t num_groups, void* out, int out_dtype,
+                                    const int64_t* out_strides, int64_t d_out, void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(pool_strides && scale_pool_strides, "kvq_dequantize_paged: null stride array");
+  PageMap pm;
+  const int rc = page_map("kvq_dequantize_paged", block_table, table_stride, table_cols, num_blocks,
+                          page_size, B, &pm);
+  if (rc != KVQ_OK) return rc;
+  const int64_t ps[3] = {0, pool_strides[0], pool_strides[1]};
+  const int64_t ss[3] = {0, scale_pool_strides[0], scale_pool_strides[1]};
+  return dequantize_impl(packed_pool, ps, scale_pool, scale_dtype, ss, B, H, S, group_size,
+                         num_groups, out, out_dtype, out_strides, d_out, pm, stream);
 }

@@ -31,6 +31,10 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_attn_workspace_bytes",
     "kvq_decode_attn",
     "kvq_decode_step",
+    "kvq_quantize_paged",
+    "kvq_dequantize_paged",
+    "kvq_decode_attn_paged",
+    "kvq_decode_step_paged",
 )
 
 _lock = threading.Lock()
@@ -83,6 +87,40 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i32,
         _vp, _i64p,
         _i64, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, ctypes.c_float,
+        _i64, _vp, _i64, _vp,
+    ]
+    # paged counterparts: (block_table, table_stride, table_cols, num_blocks,
+    # page_size) after the cache arguments; pool strides are (head, row)
+    pg = [_vp, _i64, _i64, _i64, _i64]
+    lib.kvq_quantize_paged.restype = _i32
+    lib.kvq_quantize_paged.argtypes = [
+        _vp, _i32, _i64p, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64p, _vp, _i32, _i64p, *pg, _vp, _i64, _vp,
+    ]
+    lib.kvq_dequantize_paged.restype = _i32
+    lib.kvq_dequantize_paged.argtypes = [
+        _vp, _i64p, _vp, _i32, _i64p, *pg,
+        _i64, _i64, _i64, _i64, _i64, _vp, _i32, _i64p, _i64, _vp,
+    ]
+    lib.kvq_decode_attn_paged.restype = _i32
+    lib.kvq_decode_attn_paged.argtypes = [
+        _vp, _i32, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _i32, *pg,
+        _vp, _i64p,
+        _i64, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i32, ctypes.c_float,
+        _i64, _vp, _i64, _vp,
+    ]
+    lib.kvq_decode_step_paged.restype = _i32
+    lib.kvq_decode_step_paged.argtypes = [
+        _vp, _i32, _i64p,
+        _vp, _i64p, _vp, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _i32, *pg,
+        _vp, _i64p,
+        _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, ctypes.c_float,
         _i64, _vp, _i64, _vp,
     ]

@@ -24,6 +24,7 @@ from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 from transformers.models.gpt2.modeling_gpt2 import GPT2Attention, eager_attention_forward
 
 from .attention_quant import attention_forward_quant
+from ..paged_cache import PagedQuantizedKVCache
 from .kv_cache import QuantizedKVCache
 
 
@@ -46,11 +47,12 @@ class GPT2AttentionQuantized(GPT2Attention):
         **kwargs,
     ):
         is_cross_attention = encoder_hidden_states is not None
-        quant_cache = past_key_values if isinstance(past_key_values, QuantizedKVCache) else None
+        quant_types = (QuantizedKVCache, PagedQuantizedKVCache)
+        quant_cache = past_key_values if isinstance(past_key_values, quant_types) else None
         if quant_cache is None or is_cross_attention:
             return super().forward(
                 hidden_states,
-                past_key_values=None if isinstance(past_key_values, QuantizedKVCache) else past_key_values,
+                past_key_values=None if isinstance(past_key_values, quant_types) else past_key_values,
                 attention_mask=attention_mask,
                 encoder_hidden_states=encoder_hidden_states,
                 encoder_attention_mask=encoder_attention_mask,
@@ -84,6 +86,12 @@ class GPT2AttentionQuantized(GPT2Attention):
             attn_output, attn_weights = self._upcast_and_reordered_attn(
                 query_states, k_full.to(query_states.dtype), v_full.to(query_states.dtype), attention_mask
             )
+        elif attention_mask is None and isinstance(quant_cache, PagedQuantizedKVCache):
+            attn_output = quant_cache.attend(
+                query_states, self.layer_idx, n_kv_heads=query_states.shape[1], scale=self.scaling,
+                is_causal=query_states.shape[-2] > 1,
+            ).transpose(1, 2)
+            attn_weights = None
         elif attention_mask is None:
             k_packed, k_scales, v_packed, v_scales = quant_cache.get_quantized(self.layer_idx)
             q_in = query_states if query_states.dtype in (torch.float16, torch.float32) else query_states.float()

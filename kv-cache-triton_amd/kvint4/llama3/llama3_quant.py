@@ -34,6 +34,7 @@ from transformers.models.llama.modeling_llama import (
 )
 
 from .attention_quant import attention_forward_quant_gqa
+from ..paged_cache import PagedQuantizedKVCache
 from .kv_cache import QuantizedKVCache
 
 
@@ -64,7 +65,7 @@ class LlamaAttentionQuantized(LlamaAttention):
         cos, sin = position_embeddings
         query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
 
-        if isinstance(past_key_values, QuantizedKVCache):
+        if isinstance(past_key_values, (QuantizedKVCache, PagedQuantizedKVCache)):
             cache = past_key_values
             if attention_mask is None and query_states.shape[-2] == 1:
                 # decode: append + attention in one launch
@@ -76,6 +77,13 @@ class LlamaAttentionQuantized(LlamaAttention):
                     attn_output = attn_output.transpose(1, 2).reshape(*input_shape, -1).contiguous()
                     return self.o_proj(attn_output), None
             cache.append(key_states, value_states, self.layer_idx)
+            if attention_mask is None and isinstance(cache, PagedQuantizedKVCache):
+                attn_output = cache.attend(
+                    query_states, self.layer_idx, n_kv_heads=self.config.num_key_value_heads,
+                    scale=self.scaling, is_causal=query_states.shape[-2] > 1,
+                )
+                attn_output = attn_output.transpose(1, 2).reshape(*input_shape, -1).contiguous()
+                return self.o_proj(attn_output), None
             if attention_mask is None:
                 k_packed, k_scales, v_packed, v_scales = cache.get_quantized(self.layer_idx)
                 attn_output = attention_forward_quant_gqa(

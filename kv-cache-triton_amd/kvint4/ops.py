@@ -404,11 +404,29 @@ def dense_attention_over_quantized(
     dequantize of the INT4 cache, then dense SDPA. Causal masking is aligned to
     the bottom-right corner (query i sees keys j <= Sk - Sq + i), as in the
     reference kernel (kernels/llama3/attention_quant.py:91-97,123)."""
+    D = q.shape[-1]
+    k = dequantize(k_packed, k_scales, group_size, D, q.dtype)
+    v = dequantize(v_packed, v_scales, group_size, D, q.dtype)
+    return dense_attention(q, k, v, n_kv_heads=n_kv_heads, is_causal=is_causal, sm_scale=sm_scale,
+                           seq_lens=seq_lens)
+
+
+def dense_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    n_kv_heads: int,
+    is_causal: bool,
+    sm_scale: float,
+    seq_lens: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Dense SDPA of q [B, Hq, Sq, D] over dequantized k, v [B, Hkv, Sk, D]
+    with the fused kernel's conventions: GQA head map h // (Hq / Hkv), keys
+    past seq_lens[b] masked, causal aligned bottom-right, rows with no
+    admissible key zero."""
     B, Hq, Sq, D = q.shape
-    Sk = k_packed.shape[2]
-    deq_dtype = q.dtype
-    k = dequantize(k_packed, k_scales, group_size, D, deq_dtype)
-    v = dequantize(v_packed, v_scales, group_size, D, deq_dtype)
+    Sk = k.shape[2]
     ratio = Hq // n_kv_heads
     if ratio > 1:
         k = k.repeat_interleave(ratio, dim=1)
@@ -466,3 +484,271 @@ def attention_over_quantized(
         n_kv_heads=n_kv_heads, group_size=group_size, is_causal=is_causal,
         sm_scale=sm_scale, seq_lens=seq_lens,
     )
+
+
+# ---------------------------------------------------------------------------
+# paged caches
+
+
+class PageTable:
+    """A block table for paged caches: device int32 [B, cols] of block ids
+    (-1: no block) for pages of `page_size` rows (a power of two) in pools of
+    `num_blocks` blocks. Token t of sequence b lives in pool row
+    table[b, t // page_size] * page_size + t % page_size."""
+
+    __slots__ = ("table", "page_size", "num_blocks")
+
+    def __init__(self, table: torch.Tensor, page_size: int, num_blocks: int) -> None:
+        if table.dtype != torch.int32 or table.dim() != 2 or not table.is_cuda or table.stride(-1) != 1:
+            raise ValueError("block table must be a device int32 [B, cols] tensor with contiguous rows")
+        if page_size < 1 or page_size & (page_size - 1):
+            raise ValueError("page_size must be a power of two")
+        self.table, self.page_size, self.num_blocks = table, int(page_size), int(num_blocks)
+
+    def args(self) -> tuple:
+        return (self.table.data_ptr(), self.table.stride(0), self.table.shape[1], self.num_blocks, self.page_size)
+
+    @property
+    def capacity(self) -> int:
+        return self.table.shape[1] * self.page_size
+
+
+def _check_pool(pool: torch.Tensor, scales: torch.Tensor, pt: PageTable, H: int, D: int, group_size: int) -> None:
+    rows = pt.num_blocks * pt.page_size
+    if pool.dim() != 3 or scales.dim() != 3 or pool.shape[:2] != (H, rows) or scales.shape[:2] != (H, rows):
+        raise ValueError(f"pools must be [H={H}, num_blocks*page_size={rows}, .] (got {tuple(pool.shape)}, "
+                         f"{tuple(scales.shape)})")
+    if pool.dtype != torch.uint8 or scales.dtype not in SUPPORTED_FLOATS:
+        raise ValueError("pool dtypes must be uint8 codes and float scales")
+    if pool.shape[-1] < packed_width(D, group_size) or scales.shape[-1] < num_groups(D, group_size):
+        raise ValueError("pool rows are too small for this head dim / group size")
+    if pool.stride(-1) != 1 or scales.stride(-1) != 1:
+        raise ValueError("pool rows must be contiguous")
+
+
+def quantize_into_paged(
+    x: torch.Tensor,
+    pool: torch.Tensor,
+    scales: torch.Tensor,
+    pt: PageTable,
+    group_size: int,
+    write_pos: int | torch.Tensor = 0,
+) -> None:
+    """quantize_into for a paged cache: row (b, h, s) of x [B, H, S, D] goes to
+    sequence b's position pos_b + s, i.e. its page's pool row; positions whose
+    page has no block are dropped."""
+    _check_cuda(x, pool, scales, pt.table, what="quantize_into_paged")
+    if x.dim() != 4:
+        raise ValueError("quantize_into_paged expects 4D x")
+    B, H, S, D = x.shape
+    if pt.table.shape[0] < B:
+        raise ValueError("block table has fewer rows than the batch")
+    _check_pool(pool, scales, pt, H, D, group_size)
+    wp_ptr, wp0 = None, 0
+    if isinstance(write_pos, torch.Tensor):
+        if write_pos.dtype != torch.int32 or write_pos.numel() != B or not write_pos.is_cuda:
+            raise ValueError("write_pos must be a device int32 tensor of shape [B]")
+        write_pos = write_pos.contiguous()
+        wp_ptr = write_pos.data_ptr()
+    else:
+        wp0 = int(write_pos)
+        if wp0 < 0:
+            raise ValueError("write position must be >= 0")
+    lib = nat.lib()
+    with nat.device_of(x):
+        rc = lib.kvq_quantize_paged(
+            x.data_ptr(), nat.DTYPE_CODE[x.dtype], nat.i64_array(x.stride()),
+            B, H, S, D, group_size,
+            pool.data_ptr(), nat.i64_array(pool.stride()[:2]),
+            scales.data_ptr(), nat.DTYPE_CODE[scales.dtype], nat.i64_array(scales.stride()[:2]),
+            *pt.args(), wp_ptr, wp0, nat.stream_handle(x.device),
+        )
+    nat.check(rc, "kvq_quantize_paged")
+
+
+def dequantize_paged(
+    pool: torch.Tensor,
+    scales: torch.Tensor,
+    pt: PageTable,
+    B: int,
+    S: int,
+    group_size: int,
+    d_out: int,
+    out_dtype: torch.dtype,
+) -> torch.Tensor:
+    """[B, H, S, d_out] of the first S positions of every sequence (positions
+    whose page has no block come out as zeros)."""
+    _check_cuda(pool, scales, pt.table, what="dequantize_paged")
+    if pt.table.shape[0] < B:
+        raise ValueError("block table has fewer rows than the batch")
+    H, ng = pool.shape[0], scales.shape[-1]
+    d_out = min(int(d_out), ng * group_size)
+    out = torch.empty((B, H, S, d_out), dtype=out_dtype, device=pool.device)
+    if out.numel() == 0:
+        return out
+    lib = nat.lib()
+    with nat.device_of(pool):
+        rc = lib.kvq_dequantize_paged(
+            pool.data_ptr(), nat.i64_array(pool.stride()[:2]),
+            scales.data_ptr(), nat.DTYPE_CODE[scales.dtype], nat.i64_array(scales.stride()[:2]),
+            *pt.args(), B, H, S, group_size, ng,
+            out.data_ptr(), nat.DTYPE_CODE[out_dtype], nat.i64_array(out.stride()), d_out,
+            nat.stream_handle(pool.device),
+        )
+    nat.check(rc, "kvq_dequantize_paged")
+    return out
+
+
+def _plan(lib, q: torch.Tensor, B: int, Hq: int, n_kv_heads: int, Sq: int, D: int, s_max: int,
+          sd: int, n_split: int | None) -> tuple[int, int]:
+    qd = nat.DTYPE_CODE[q.dtype]
+    if n_split is None:
+        n_split = lib.kvq_decode_attn_num_splits(B, Hq, n_kv_heads, Sq, D, s_max, qd, sd, _num_cus(q.device))
+        if n_split < 0:
+            nat.check(int(n_split), "kvq_decode_attn_num_splits")
+    elif n_split < 1:
+        raise ValueError("n_split must be >= 1")
+    ws_bytes = lib.kvq_decode_attn_workspace_bytes(B, Hq, n_kv_heads, Sq, D, qd, sd, n_split)
+    if ws_bytes < 0:
+        nat.check(int(ws_bytes), "kvq_decode_attn_workspace_bytes")
+    return int(n_split), int(ws_bytes)
+
+
+def fused_decode_attention_paged(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_pool: torch.Tensor,
+    v_scales: torch.Tensor,
+    pt: PageTable,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    is_causal: bool,
+    sm_scale: float,
+    seq_lens: torch.Tensor | None = None,
+    seq_len: int | None = None,
+    out: torch.Tensor | None = None,
+    n_split: int | None = None,
+) -> torch.Tensor:
+    """fused_decode_attention over a paged cache. Sequence b attends its first
+    seq_lens[b] tokens (device int32 [B]) or `seq_len` tokens. Raises
+    KVQUnsupported where the kernel does not apply (fp32 queries or scales,
+    page_size < 64)."""
+    _check_cuda(q, k_pool, k_scales, v_pool, v_scales, pt.table, what="fused_decode_attention_paged")
+    B, Hq, Sq, D = q.shape
+    if pt.table.shape[0] < B:
+        raise ValueError("block table has fewer rows than the batch")
+    for pool, sc in ((k_pool, k_scales), (v_pool, v_scales)):
+        _check_pool(pool, sc, pt, n_kv_heads, D, group_size)
+    if out is None:
+        out = torch.empty_like(q)
+    if v_scales.dtype != k_scales.dtype:
+        raise ValueError("K and V scale pools must share a dtype")
+    sl_ptr, s_max = None, pt.capacity
+    if seq_lens is not None:
+        if seq_lens.dtype != torch.int32 or not seq_lens.is_cuda or seq_lens.numel() != B:
+            raise ValueError("seq_lens must be a device int32 tensor of shape [B]")
+        seq_lens = seq_lens.contiguous()
+        sl_ptr, seq_len = seq_lens.data_ptr(), 0
+    else:
+        if seq_len is None or not 0 <= int(seq_len) <= pt.capacity:
+            raise ValueError(f"seq_len must be in [0, {pt.capacity}] when seq_lens is not given")
+        seq_len = int(seq_len)
+        s_max = seq_len
+    lib = nat.lib()
+    sd = nat.DTYPE_CODE[k_scales.dtype]
+    n_split, ws_bytes = _plan(lib, q, B, Hq, n_kv_heads, Sq, D, s_max, sd, n_split)
+    with nat.device_of(q):
+        stream = nat.stream_handle(q.device)
+        ws_ptr, ws_len = None, 0
+        if ws_bytes > 0:
+            ws = _workspaces.get(q.device, stream, ws_bytes)
+            ws_ptr, ws_len = ws.data_ptr(), ws.numel()
+        rc = lib.kvq_decode_attn_paged(
+            q.data_ptr(), nat.DTYPE_CODE[q.dtype], nat.i64_array(q.stride()),
+            k_pool.data_ptr(), nat.i64_array(k_pool.stride()[:2]),
+            k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:2]),
+            v_pool.data_ptr(), nat.i64_array(v_pool.stride()[:2]),
+            v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:2]),
+            sd, *pt.args(),
+            out.data_ptr(), nat.i64_array(out.stride()),
+            B, Hq, n_kv_heads, Sq, D, group_size,
+            sl_ptr, seq_len, 1 if is_causal else 0, float(sm_scale),
+            n_split, ws_ptr, ws_len, stream,
+        )
+    nat.check(rc, "kvq_decode_attn_paged")
+    return out
+
+
+def decode_step_paged(
+    q: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_pool: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_pool: torch.Tensor,
+    v_scales: torch.Tensor,
+    pt: PageTable,
+    position,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    sm_scale: float,
+    out: torch.Tensor | None = None,
+    n_split: int | None = None,
+) -> torch.Tensor:
+    """decode_step over a paged cache: the new token of sequence b goes to its
+    position (int, or device int32 [B] of old lengths) through the block table;
+    a position whose page has no block is neither written nor attended."""
+    _check_cuda(q, k_new, v_new, k_pool, pt.table, what="decode_step_paged")
+    B, Hq, Sq, D = q.shape
+    if pt.table.shape[0] < B:
+        raise ValueError("block table has fewer rows than the batch")
+    for pool, sc in ((k_pool, k_scales), (v_pool, v_scales)):
+        _check_pool(pool, sc, pt, n_kv_heads, D, group_size)
+    if Sq != 1:
+        raise nat.KVQUnsupported("decode_step_paged handles one query position")
+    if out is None:
+        out = torch.empty_like(q)
+    if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+        raise nat.KVQUnsupported("decode_step_paged needs K/V rows in q's dtype")
+    if k_new.stride(-1) != 1:
+        k_new = k_new.contiguous()
+    if v_new.stride(-1) != 1:
+        v_new = v_new.contiguous()
+    cap = pt.capacity
+    if isinstance(position, torch.Tensor):
+        if position.dtype != torch.int32 or not position.is_cuda or position.numel() != B:
+            raise ValueError("position must be an int or a device int32 tensor of shape [B]")
+        pos_ptr, pos0, s_max = position.contiguous().data_ptr(), 0, cap
+    else:
+        pos_ptr, pos0 = None, int(position)
+        if not 0 <= pos0 < cap:
+            raise ValueError(f"write position {pos0} outside the table's capacity {cap}")
+        s_max = pos0 + 1
+    lib = nat.lib()
+    sd = nat.DTYPE_CODE[k_scales.dtype]
+    n_split, ws_bytes = _plan(lib, q, B, Hq, n_kv_heads, 1, D, s_max, sd, n_split)
+    with nat.device_of(q):
+        stream = nat.stream_handle(q.device)
+        ws_ptr, ws_len = None, 0
+        if ws_bytes > 0:
+            ws = _workspaces.get(q.device, stream, ws_bytes)
+            ws_ptr, ws_len = ws.data_ptr(), ws.numel()
+        rc = lib.kvq_decode_step_paged(
+            q.data_ptr(), nat.DTYPE_CODE[q.dtype], nat.i64_array(q.stride()),
+            k_new.data_ptr(), nat.i64_array(k_new.stride()),
+            v_new.data_ptr(), nat.i64_array(v_new.stride()),
+            k_pool.data_ptr(), nat.i64_array(k_pool.stride()[:2]),
+            k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:2]),
+            v_pool.data_ptr(), nat.i64_array(v_pool.stride()[:2]),
+            v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:2]),
+            sd, *pt.args(),
+            out.data_ptr(), nat.i64_array(out.stride()),
+            B, Hq, n_kv_heads, D, group_size,
+            pos_ptr, pos0, float(sm_scale),
+            n_split, ws_ptr, ws_len, stream,
+        )
+    nat.check(rc, "kvq_decode_step_paged")
+    return out
