@@ -149,6 +149,32 @@ class PagedQuantizedKVCache:
             self._lens[idx][b] = 0
             self._seq_lens[idx][b] = 0
 
+    def _load_layer(self, layer_idx: int, parts: list[torch.Tensor], lens: list[int], d_head: int) -> None:
+        """Install already-quantized rows ([B, H_kv, S, .] codes and scales of
+        every sequence, its first lens[b] rows valid) as layer `layer_idx`."""
+        kp, ks = parts[0], parts[1]
+        B, H, S, _ = kp.shape
+        if self._shape is None:
+            self._shape = (B, H, d_head, ks.dtype, self._scale_dtype or ks.dtype, kp.device)
+            self._pages = [[] for _ in range(B)]
+            self._grow_pool(self._init_blocks)
+        if self._shape[:3] != (B, H, d_head) or self._shape[4] != ks.dtype:
+            raise ValueError("stored layer does not match the cache's shape or scale dtype")
+        if layer_idx in self._pools and any(self._lens[layer_idx]):
+            raise ValueError(f"layer {layer_idx} already holds state")
+        self._layer(layer_idx)
+        self._ensure_pages(lens)
+        pools = self._pools[layer_idx]
+        pt = self._page_table()
+        t = torch.arange(S, device=kp.device)
+        page = pt.table[:, (t // self.page_size).clamp(max=pt.table.shape[1] - 1)].to(torch.int64)
+        rows = page.clamp(min=0) * self.page_size + (t % self.page_size)[None, :]      # [B, S]
+        valid = t[None, :] < torch.tensor(lens, device=kp.device)[:, None]            # [B, S]
+        for pool, src in zip(pools, parts):
+            pool[:, rows[valid]] = src.permute(1, 0, 2, 3)[:, valid]
+        self._lens[layer_idx] = list(lens)
+        self._seq_lens[layer_idx].copy_(torch.tensor(lens, dtype=torch.int32))
+
     # -- appends -------------------------------------------------------------
     def append(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> None:
         """Quantize [B, H_kv, S, d] K/V and append them after each sequence's
