@@ -428,6 +428,18 @@ def dense_attention(
     B, Hq, Sq, D = q.shape
     Sk = k.shape[2]
     ratio = Hq // n_kv_heads
+    if (ratio > 1 and seq_lens is None and not (is_causal and Sq != Sk)
+            and q.dtype in (torch.bfloat16, torch.float16)):
+        # the fused SDPA kernels read each KV head for its whole query group
+        # (no GQA-expanded copy of K/V)
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return F.scaled_dot_product_attention(q, k, v, is_causal=is_causal, scale=sm_scale,
+                                                      enable_gqa=True)
+        except RuntimeError:
+            pass
     if ratio > 1:
         k = k.repeat_interleave(ratio, dim=1)
         v = v.repeat_interleave(ratio, dim=1)
