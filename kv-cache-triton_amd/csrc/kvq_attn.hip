@@ -1297,11 +1297,15 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   const int last_tok = L > 0 ? L - 1 : 0;
 
   for (int base = wave; base < ntiles; base += 4 * CH) {
+    // tiles of this chunk the wave has (wave-uniform): a split's last chunk
+    // may hold fewer than CH, and the rest are neither loaded nor computed
+    const int nv = min(CH, (ntiles - base + 3) / 4);
     uint4 kcode[CH];
     uint32_t vcode[CH][4];
     float sk[CH], sv[CH];
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
+      if (i >= nv) break;
       const int t0 = t_begin + (base + 4 * i) * TPT;
       const uint32_t tk = (uint32_t)min(t0 + kt, last_tok);
       kcode[i] = *(const uint4*)(kp_bh + (tk * kps + 16u * kc));
@@ -1317,6 +1321,11 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     float s[CH][ROWS];
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
+      if (i >= nv) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) s[i][r] = kNeg;
+        continue;
+      }
       const int t = t_begin + (base + 4 * i) * TPT + kt;
       const bool tv_ok = (base + 4 * i < ntiles) && (t < t_end);
       float acc[ROWS];
@@ -1389,6 +1398,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     const int pos = (kt % VTS) * 4 + kt / VTS;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
+      if (i >= nv) break;
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) {
         const float p = s[i][r] > kNeg ? __builtin_amdgcn_exp2f(s[i][r] - m_run[r]) : 0.0f;
@@ -1404,6 +1414,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
 
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
+      if (i >= nv) break;
       if constexpr (DOT2) {
         uint32_t cp01[8], cp23[8];
         const uint32_t plo01 = __builtin_amdgcn_perm(vcode[i][1], vcode[i][0], 0x05040100u);
@@ -1484,7 +1495,13 @@ static bool use_mfma(int q_dtype, int scale_dtype) {
 
 // Fewest keys a split is given (when the sequence is long enough to split):
 // two 64-token MFMA tiles, or four 16/32-token VALU tiles.
-static int64_t min_split_tokens(bool mfma, int64_t D) { return mfma ? 128 : 4 * (64 / (D / 32)); }
+// Shortest split worth its share of the cross-split merge (measured): the
+// matrix-core kernel runs a 64-key tile per wave in well under the merge's
+// cost, the exact-fp32 VALU kernel needs about 1024 keys per split.
+static int64_t min_split_tokens(bool mfma, int64_t D) {
+  (void)D;
+  return mfma ? 128 : 1024;
+}
 
 // Split-K plan: enough splits that B * Hkv * row_chunks * n_split workgroups
 // cover the CUs once (one resident workgroup per CU), no split shorter than
@@ -1636,10 +1653,11 @@ extern "C" int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_
     set_error("kvq_decode_attn_workspace_bytes: bad dtype or n_split");
     return KVQ_EINVAL;
   }
-  // s_max only bounds n_split in planning; pass one that keeps n_split.
+  // s_max only bounds n_split in planning; pass one long enough that every
+  // split reaches min_split_tokens, so the plan keeps n_split.
   Plan p;
-  const int rc =
-      make_plan(B, Hq, Hkv, Sq, D, n_split * 256, q_dtype, scale_dtype, n_split, 1, &p);
+  const int rc = make_plan(B, Hq, Hkv, Sq, D, n_split * min_split_tokens(use_mfma(q_dtype, scale_dtype), D),
+                           q_dtype, scale_dtype, n_split, 1, &p);
   if (rc != KVQ_OK) {
     set_error("kvq_decode_attn_workspace_bytes: unsupported or invalid shape");
     return rc;

@@ -47,8 +47,9 @@ def test_num_splits_planning():
     assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 100, B16, B16, 256) == 1
     # plenty of units already -> one split
     assert lib.kvq_decode_attn_num_splits(16, 25, 25, 1, 64, 1024, F16, F16, 256) == 1
-    # fp32 queries plan for the VALU kernel (32-token tiles at D=64)
-    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 1024, F32, F16, 256) == 8
+    # fp32 queries plan for the VALU kernel: no split shorter than 1024 keys
+    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 1024, F32, F16, 256) == 1
+    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 16384, F32, F16, 256) == 16
     assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 96, 1024, B16, B16, 256) == nat.KVQ_EUNSUP
     assert lib.kvq_decode_attn_num_splits(1, 30, 8, 1, 128, 1024, B16, B16, 256) == nat.KVQ_EINVAL
 
@@ -56,6 +57,10 @@ def test_num_splits_planning():
 def test_workspace_bytes():
     lib = nat.lib()
     B16 = nat.KVQ_BF16
+    # a requested split count is kept whatever the kernel's minimum split
+    # length (the VALU kernel's is 1024 keys): 12 units x 3 splits of partials
+    ws3 = lib.kvq_decode_attn_workspace_bytes(1, 12, 12, 1, 64, nat.KVQ_F32, nat.KVQ_F16, 3)
+    assert ws3 == 1024 * 5 * 64 + 512 + 12 * 3 * 64 * 4  # counters, (max, sum) pairs padded to 256 B, partials
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 1) == 0
     ws = lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 32)
     # counter block (1024 units x 5 counters x 64 bytes), then 8 units x 32 splits x 4 rows x (128 + 2) floats
