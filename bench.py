@@ -108,7 +108,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); the INT4 decode "
-              "path is measured on one MI355X. See the sharding note in DESIGN.md.", file=sys.stderr)
+              "path is measured on one MI355X (a multi-GPU run would shard KV heads across GPUs with no "
+              "exchange inside attention).", file=sys.stderr)
         return 2
 
     import numpy as np

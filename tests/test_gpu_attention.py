@@ -1,6 +1,6 @@
 """GPU parity: fused INT4 decode attention vs the CPU oracle.
 
-Bars:
+Bars (the parity targets of this path):
   * bf16 / fp16 inputs: max-abs <= 2e-2 against the reference's own oracle as
     written (dequantize to the scale dtype, repeat_interleave over the GQA
     group, SDPA in the input dtype — tests/llama3/test_attention_quant_gqa.py:
