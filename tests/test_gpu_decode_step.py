@@ -141,3 +141,33 @@ def test_decode_step_rejects_bad_position_and_unsupported():
         ops.decode_step(q, kn, vn, *a, 64, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
     with pytest.raises(ops.nat.KVQUnsupported):
         ops.decode_step(q.float(), kn.float(), vn.float(), *a, 10, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
+
+
+def test_decode_step_in_hip_graph_replays():
+    """The decode step captured in a HIP graph: every replay (with eager work
+    and synchronisation between them) gives the eager result and the same
+    cache bytes; the split-merge counters are re-armed by the kernel itself
+    (no memset node in the graph)."""
+    B, Hq, Hkv, D, G, pos = 1, 32, 8, 128, 32, 5000
+    a = _cache(B, Hkv, pos + 64, D, G, "bf16", pos, seed=21)
+    q, kn, vn = _new(B, Hq, Hkv, D, "bf16", seed=21)
+    sm = D ** -0.5
+    out = torch.empty_like(q)
+    ops.decode_step(q, kn, vn, *a, pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm, out=out)  # warm-up
+    torch.cuda.synchronize()
+    want = out.clone()
+    cache_want = [t.clone() for t in a]
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        ops.decode_step(q, kn, vn, *a, pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm, out=out)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        out.zero_()
+        (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        for x, y in zip(a, cache_want):
+            assert torch.equal(x, y)
