@@ -109,64 +109,102 @@ __device__ __forceinline__ float dpp_f(float v) {
                                                                0xF, 0xF, false));
 }
 
-template <int XDT, int LPG>  // LPG = lanes per group = G / 8
-__global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t cpr = a.D >> 3;  // chunks per row
-  const bool live = idx < a.rows * cpr;
-  const int64_t row = live ? idx / cpr : 0;
-  const int64_t ch = live ? idx - row * cpr : 0;
-  const int64_t s = row % a.S;
-  const int64_t bh = row / a.S;
-  const int64_t h = bh % a.H;
-  const int64_t b = bh / a.H;
-  const int64_t xoff = b * a.xs_b + h * a.xs_h + s * a.xs_s + 8 * ch;
+// rint(x / s) where x / s is the IEEE (correctly rounded) fp32 quotient, for
+// |x| <= 7 s (x an element of the group whose absmax / 7 is s, s normal):
+// t = x * (1 / s), both steps correctly rounded, lies within 2^-19.6 of the
+// rounded quotient (relative error 2^-23 on |x / s| <= 7, plus the quotient's
+// own rounding of 2^-21), so rint(t) is rint of the quotient unless t is
+// within that distance of a half-integer; those rare elements (and groups
+// whose scale is not a moderate normal number) take the division itself. The
+// threshold used, 2^-17, leaves a margin of 6x.
+__device__ __forceinline__ float rint_quotient(float x, float s, float inv, bool fast) {
+  const float t = x * inv;
+  const float r = __builtin_rintf(t);
+  if (fast && !(fabsf(t - r) > 0.5f - 0x1p-17f)) return r;
+  return __builtin_rintf(x / s);
+}
 
-  float x[8];
-  if constexpr (XDT == KVQ_F32) {
-    const float4 lo = *(const float4*)((const float*)a.x + xoff);
-    const float4 hi = *(const float4*)((const float*)a.x + xoff + 4);
-    x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
-    x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
-  } else {
-    const uint4 w = *(const uint4*)((const uint16_t*)a.x + xoff);
-    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+// Each thread takes chunk ch of RPT rows (row slot r0 and r0 + k * rq): its
+// loads for all of them are in flight together, and for every k the G/8
+// lanes of a group still hold adjacent chunks of one row. Index arithmetic
+// is 32-bit (the host takes this path only when rows * D / 8 < 2^32).
+constexpr int kQuantRows = 4;  // rows per thread of the vector quantize / dequantize kernels
+
+template <int XDT, int LPG, int RPT>  // LPG = lanes per group = G / 8
+__global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
+  const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t cpr = (uint32_t)a.D >> 3;  // chunks per row
+  const uint32_t rows = (uint32_t)a.rows;
+  const uint32_t rq = (rows + RPT - 1) / RPT;
+  const bool slot = idx < rq * cpr;
+  const uint32_t r0 = slot ? idx / cpr : 0u;
+  const uint32_t ch = slot ? idx - r0 * cpr : 0u;
+  const uint32_t S = (uint32_t)a.S, H = (uint32_t)a.H;
+
+  float x[RPT][8];
+  bool live[RPT];
+  uint32_t bb[RPT], hh[RPT], ss[RPT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (XDT == KVQ_BF16) {
-        x[2 * j] = bf16_bits_to_f32(wd[j] & 0xffffu);
-        x[2 * j + 1] = bf16_bits_to_f32(wd[j] >> 16);
-      } else {
-        x[2 * j] = f16_bits_to_f32(wd[j] & 0xffffu);
-        x[2 * j + 1] = f16_bits_to_f32(wd[j] >> 16);
+  for (int k = 0; k < RPT; ++k) {
+    const uint32_t row = r0 + (uint32_t)k * rq;
+    live[k] = slot && row < rows;
+    const uint32_t rw = live[k] ? row : 0u;
+    ss[k] = rw % S;
+    const uint32_t bh = rw / S;
+    hh[k] = bh % H;
+    bb[k] = bh / H;
+    const int64_t xoff = (int64_t)bb[k] * a.xs_b + (int64_t)hh[k] * a.xs_h + (int64_t)ss[k] * a.xs_s + 8 * ch;
+    if constexpr (XDT == KVQ_F32) {
+      const float4 lo = *(const float4*)((const float*)a.x + xoff);
+      const float4 hi = *(const float4*)((const float*)a.x + xoff + 4);
+      x[k][0] = lo.x; x[k][1] = lo.y; x[k][2] = lo.z; x[k][3] = lo.w;
+      x[k][4] = hi.x; x[k][5] = hi.y; x[k][6] = hi.z; x[k][7] = hi.w;
+    } else {
+      const uint4 w = *(const uint4*)((const uint16_t*)a.x + xoff);
+      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (XDT == KVQ_BF16) {
+          x[k][2 * j] = bf16_bits_to_f32(wd[j] & 0xffffu);
+          x[k][2 * j + 1] = bf16_bits_to_f32(wd[j] >> 16);
+        } else {
+          x[k][2 * j] = f16_bits_to_f32(wd[j] & 0xffffu);
+          x[k][2 * j + 1] = f16_bits_to_f32(wd[j] >> 16);
+        }
       }
     }
   }
-  float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
-  // Every lane of the wave takes part in the DPP steps (dead lanes carry 0).
-  if constexpr (LPG >= 2) amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
-  if constexpr (LPG >= 4) amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
-  if constexpr (LPG >= 8) amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
-  if constexpr (LPG >= 16) amax = fmaxf(amax, dpp_f<0x140>(amax)); // row_mirror
-  if (!live) return;
-  // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
-  const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
-  uint32_t word = 0;
+  for (int k = 0; k < RPT; ++k) {
+    float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float qf = __builtin_rintf(x[e] / scale);  // round half to even
-    qf = fminf(fmaxf(qf, -8.0f), 7.0f);
-    word |= (uint32_t)((int)qf + 8) << (4 * e);
-  }
-  const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s);
-  if (pos < 0) return;  // paged: no block holds this position
-  // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
-  *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
-  if (ch % LPG == 0) {
-    const int64_t g = ch / LPG;
-    store_from_f32(a.scales, b * a.ss_b + h * a.ss_h + pos * a.ss_s + g, a.scale_dtype, scale);
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[k][e]));
+    // Every lane of the wave takes part in the DPP steps (dead lanes carry 0).
+    if constexpr (LPG >= 2) amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+    if constexpr (LPG >= 4) amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+    if constexpr (LPG >= 8) amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
+    if constexpr (LPG >= 16) amax = fmaxf(amax, dpp_f<0x140>(amax)); // row_mirror
+    if (!live[k]) continue;
+    // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
+    const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float qf = rint_quotient(x[k][e], scale, inv, fast);  // round half to even
+      qf = fminf(fmaxf(qf, -8.0f), 7.0f);
+      word |= (uint32_t)((int)qf + 8) << (4 * e);
+    }
+    const int64_t b = bb[k], h = hh[k];
+    const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + ss[k]);
+    if (pos < 0) continue;  // paged: no block holds this position
+    // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
+    *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
+    if (ch % LPG == 0) {
+      const int64_t g = ch / LPG;
+      store_from_f32(a.scales, b * a.ss_b + h * a.ss_h + pos * a.ss_s + g, a.scale_dtype, scale);
+    }
   }
 }
 
@@ -208,6 +246,73 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
     const uint32_t nib = (k & 1) ? (byte >> 4) : (byte & 15u);
     const float v = (float)((int)nib - 8) * scale;
     store_from_f32(a.out, obase + c * a.os_d, a.out_dtype, v);
+  }
+}
+
+// Vector path: one thread per 8 consecutive elements of a row (one 4-byte
+// code word and its group's scale in, one 16-byte store of 16-bit outputs or
+// two of fp32 out). Taken when G is a multiple of 8 dividing d_out (=
+// groups * G), packed rows are 4-byte aligned and output rows have unit
+// inner stride and 16-byte aligned starts.
+template <int ODT, int RPT>
+__global__ __launch_bounds__(256) void dequantize_vec_kernel(const DequantArgs a) {
+  const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t cpr = (uint32_t)a.d_out >> 3;  // chunks per row
+  const uint32_t rows = (uint32_t)a.rows;
+  const uint32_t rq = (rows + RPT - 1) / RPT;
+  if (idx >= rq * cpr) return;
+  const uint32_t r0 = idx / cpr;
+  const uint32_t ch = idx - r0 * cpr;
+  const uint32_t S = (uint32_t)a.S, H = (uint32_t)a.H;
+  uint32_t w[RPT];
+  float sc[RPT];
+  int64_t obase[RPT];
+  bool live[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const uint32_t row = r0 + (uint32_t)k * rq;
+    live[k] = row < rows;
+    const uint32_t rw = live[k] ? row : 0u;
+    const uint32_t s = rw % S, bh = rw / S;
+    const int64_t h = bh % H, b = bh / H;
+    obase[k] = b * a.os_b + h * a.os_h + (int64_t)s * a.os_s + 8 * ch;
+    const int64_t r = a.pm.table ? page_row(a.pm, b, s) : (int64_t)s;
+    if (r < 0) {  // paged: no block holds this position -> zeros
+      w[k] = 0x88888888u;
+      sc[k] = 0.0f;
+    } else {
+      w[k] = *(const uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + r * a.ps_s + 4 * ch);
+      sc[k] = load_as_f32(a.scales, b * a.ss_b + h * a.ss_h + r * a.ss_s + (8 * ch) / a.G, a.scale_dtype);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    if (!live[k]) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)((int)((w[k] >> (4 * e)) & 15u) - 8) * sc[k];
+    const int64_t o = obase[k];
+    if constexpr (ODT == KVQ_F32) {
+      *(float4*)((float*)a.out + o) = make_float4(v[0], v[1], v[2], v[3]);
+      *(float4*)((float*)a.out + o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      // finite values: the hardware conversions round to nearest even, as
+      // f32_to_bf16_bits / f32_to_f16_bits do
+      uint32_t p[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (ODT == KVQ_BF16) {
+          typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+          const bf16x2_v h = {(__bf16)v[2 * j], (__bf16)v[2 * j + 1]};
+          p[j] = __builtin_bit_cast(uint32_t, h);
+        } else {
+          typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+          const f16x2_v h = {(_Float16)v[2 * j], (_Float16)v[2 * j + 1]};
+          p[j] = __builtin_bit_cast(uint32_t, h);
+        }
+      }
+      *(uint4*)((uint16_t*)a.out + o) = make_uint4(p[0], p[1], p[2], p[3]);
+    }
   }
 }
 
@@ -278,17 +383,18 @@ int quantize_impl(const char* who, const void* x, int x_dtype, const int64_t* x_
                    D % group_size == 0 && a.xs_d == 1 &&
                    (uintptr_t)x % 16 == 0 && (a.xs_b * esz) % 16 == 0 && (a.xs_h * esz) % 16 == 0 &&
                    (a.xs_s * esz) % 16 == 0 &&
-                   (uintptr_t)packed % 4 == 0 && a.ps_b % 4 == 0 && a.ps_h % 4 == 0 && a.ps_s % 4 == 0;
+                   (uintptr_t)packed % 4 == 0 && a.ps_b % 4 == 0 && a.ps_h % 4 == 0 && a.ps_s % 4 == 0 &&
+                   rows * (D / 8) < (1ll << 32) - 256 * kQuantRows;
   if (vec) {
-    const int64_t total = rows * (D / 8);
+    const int64_t total = (rows + kQuantRows - 1) / kQuantRows * (D / 8);
     const dim3 grid((unsigned)((total + 255) / 256));
-#define KVQ_QVEC(XDT)                                                                              \
-    switch (lpg) {                                                                                 \
-      case 1: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 1>), grid, dim3(256), 0, st, a); break;   \
-      case 2: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 2>), grid, dim3(256), 0, st, a); break;   \
-      case 4: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 4>), grid, dim3(256), 0, st, a); break;   \
-      case 8: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 8>), grid, dim3(256), 0, st, a); break;   \
-      default: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 16>), grid, dim3(256), 0, st, a); break; \
+#define KVQ_QVEC(XDT)                                                                                          \
+    switch (lpg) {                                                                                             \
+      case 1: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 1, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
+      case 2: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 2, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
+      case 4: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 4, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
+      case 8: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 8, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
+      default: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 16, kQuantRows>), grid, dim3(256), 0, st, a); break; \
     }
     switch (x_dtype) {
       case KVQ_BF16: KVQ_QVEC(KVQ_BF16) break;
@@ -340,9 +446,25 @@ int dequantize_impl(const void* packed, const int64_t* packed_strides,
   a.scale_dtype = scale_dtype; a.out_dtype = out_dtype;
   a.pm = pm;
 
+  const int64_t oes = dtype_size(out_dtype);
+  const bool vec = group_size % 8 == 0 && d_out == num_groups * group_size && a.os_d == 1 &&
+                   (uintptr_t)out % 16 == 0 && (a.os_b * oes) % 16 == 0 && (a.os_h * oes) % 16 == 0 &&
+                   (a.os_s * oes) % 16 == 0 && (uintptr_t)packed % 4 == 0 && a.ps_b % 4 == 0 &&
+                   a.ps_h % 4 == 0 && a.ps_s % 4 == 0 && rows * (d_out / 8) < (1ll << 32) - 256 * kQuantRows;
+  hipStream_t st = (hipStream_t)stream;
+  if (vec) {
+    const int64_t total = (rows + kQuantRows - 1) / kQuantRows * (d_out / 8);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    switch (out_dtype) {
+      case KVQ_BF16: hipLaunchKernelGGL((dequantize_vec_kernel<KVQ_BF16, kQuantRows>), grid, dim3(256), 0, st, a); break;
+      case KVQ_F16: hipLaunchKernelGGL((dequantize_vec_kernel<KVQ_F16, kQuantRows>), grid, dim3(256), 0, st, a); break;
+      default: hipLaunchKernelGGL((dequantize_vec_kernel<KVQ_F32, kQuantRows>), grid, dim3(256), 0, st, a); break;
+    }
+    KVQ_CHECK_LAUNCH("kvq_dequantize");
+    return KVQ_OK;
+  }
   const int64_t total = rows * num_groups;
-  hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a);
   KVQ_CHECK_LAUNCH("kvq_dequantize");
   return KVQ_OK;
 }
