@@ -1557,15 +1557,19 @@ static int64_t workspace_bytes_for(const Plan& p, int64_t D) {
 
 // Waves per workgroup of the MFMA kernel: one row set runs 8 waves (two per
 // SIMD hide each other's latency); two row sets need more registers than that
-// allows and run 4. Each wave keeps the loads of two 64-token tiles in flight.
+// allows and run 4. Tiles whose loads a wave keeps in flight: one with one row
+// set (its SIMD partner covers the latency; a second slot measured 5-12 %
+// slower from 4K to 128K keys), two with two row sets (one wave per SIMD;
+// one slot measured 8 % slower).
 template <int RS>
 constexpr int mfma_waves() { return RS == 1 ? 8 : 4; }
-constexpr int kMfmaTilesInFlight = 2;
+template <int RS>
+constexpr int mfma_tiles_in_flight() { return RS == 1 ? 1 : 2; }
 
 template <int D, int RS, int QM, int SM, bool PAGED>
 static void launch_mfma_rs(const AttnArgs& a, bool rowmask, dim3 grid, hipStream_t st) {
   constexpr int NW = mfma_waves<RS>();
-  constexpr int CH = kMfmaTilesInFlight;
+  constexpr int CH = mfma_tiles_in_flight<RS>();
   if (rowmask) hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, true, NW, CH, PAGED>), grid, dim3(64 * NW), 0, st, a);
   else hipLaunchKernelGGL((decode_attn_mfma_kernel<D, RS, QM, SM, false, NW, CH, PAGED>), grid, dim3(64 * NW), 0, st, a);
 }
