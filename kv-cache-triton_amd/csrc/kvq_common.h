@@ -36,6 +36,22 @@ __device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dt) {
   return ((const float*)p)[i];
 }
 
+// load_as_f32 of N elements, with one dtype branch around all N loads so
+// that they are in flight together.
+template <int N>
+__device__ __forceinline__ void load_n_as_f32(const void* p, const int64_t* i, int dt, float* out) {
+  if (dt == KVQ_F32) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) out[k] = ((const float*)p)[i[k]];
+    return;
+  }
+  uint32_t raw[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) raw[k] = ((const uint16_t*)p)[i[k]];
+#pragma unroll
+  for (int k = 0; k < N; ++k) out[k] = dt == KVQ_BF16 ? bf16_bits_to_f32(raw[k]) : f16_bits_to_f32(raw[k]);
+}
+
 // Store fp32 `v` into element i of a tensor of dtype `dt` (RNE narrowing).
 __device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float v) {
   if (dt == KVQ_BF16) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(v);
@@ -46,9 +62,11 @@ __device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float
 // Paged cache rows. A pool holds num_blocks blocks of 2^page_shift rows per
 // head; sequence b's token t lives in pool row
 //   table[b * tab_stride + (t >> page_shift)] << page_shift | (t & (page_size - 1)).
-// table == nullptr means the contiguous [B, H, S] layout. A table entry that
-// is negative or >= n_blocks, or a page index >= n_pages, has no row (-1).
+// paged == 0 means the contiguous [B, H, S] layout. A table entry that is
+// negative or >= n_blocks, or a page index >= n_pages, has no row (-1); the
+// table is read only where n_pages > 0 (a table with no columns may be null).
 struct PageMap {
+  int paged;
   const int32_t* table;
   int64_t tab_stride;  // int32 entries between sequences' table rows
   int64_t n_pages;     // entries of a table row in use
@@ -62,6 +80,38 @@ __device__ __forceinline__ int64_t page_row(const PageMap& m, int64_t b, int64_t
   const int64_t blk = m.table[b * m.tab_stride + p];
   if (blk < 0 || blk >= m.n_blocks) return -1;
   return (blk << m.page_shift) | (t & ((int64_t(1) << m.page_shift) - 1));
+}
+
+// page_row of N positions (sequence b[k], token t[k]) at once, with every
+// table read in flight together: each read is taken from an in-range entry
+// (column 0 for a position off the table) and the result selected after, so
+// no read waits inside a per-position branch. Contiguous layout: t itself.
+template <int N>
+__device__ __forceinline__ void page_rows(const PageMap& m, const uint32_t* b, const int64_t* t,
+                                          int64_t* out) {
+  if (!m.paged) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) out[k] = t[k];
+    return;
+  }
+  int64_t blk[N];
+  if (m.n_pages > 0) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const int64_t p = t[k] >> m.page_shift;
+      const bool on = t[k] >= 0 && p < m.n_pages;
+      blk[k] = m.table[(int64_t)b[k] * m.tab_stride + (on ? p : 0)];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; ++k) blk[k] = -1;
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int64_t p = t[k] >> m.page_shift;
+    const bool ok = t[k] >= 0 && p < m.n_pages && blk[k] >= 0 && blk[k] < m.n_blocks;
+    out[k] = ok ? (blk[k] << m.page_shift) | (t[k] & ((int64_t(1) << m.page_shift) - 1)) : -1;
+  }
 }
 
 inline int dtype_size(int dt) { return dt == KVQ_F32 ? 4 : 2; }

@@ -32,13 +32,13 @@ struct QuantArgs {
   const int32_t* write_pos;
   int64_t write_pos0;
   int x_dtype, scale_dtype;
-  PageMap pm;  // pm.table != nullptr: packed/scales are pools (ps_b = ss_b = 0)
+  PageMap pm;  // pm.paged: packed/scales are pools (ps_b = ss_b = 0)
 };
 
 // Destination row of (b, position) and whether it exists: the position
 // itself in the contiguous layout, its pool row in the paged one.
 __device__ __forceinline__ int64_t dest_row(const QuantArgs& a, int64_t b, int64_t pos) {
-  return a.pm.table ? page_row(a.pm, b, pos) : pos;
+  return a.pm.paged ? page_row(a.pm, b, pos) : pos;
 }
 
 template <int XDT>
@@ -124,11 +124,21 @@ __device__ __forceinline__ float rint_quotient(float x, float s, float inv, bool
   return __builtin_rintf(x / s);
 }
 
-// Each thread takes chunk ch of RPT rows (row slot r0 and r0 + k * rq): its
-// loads for all of them are in flight together, and for every k the G/8
-// lanes of a group still hold adjacent chunks of one row. Index arithmetic
-// is 32-bit (the host takes this path only when rows * D / 8 < 2^32).
-constexpr int kQuantRows = 4;  // rows per thread of the vector quantize / dequantize kernels
+// Each thread takes chunk ch of RPT rows (row slot r0 and r0 + k * rq); for
+// every k the G/8 lanes of a group hold adjacent chunks of one row. All of
+// its loads are issued before any store, in this order: the x chunks of the
+// RPT rows, their write positions, then (paged) the page-table entries, which
+// need the positions. Placing each row only after the previous row's loads
+// had arrived cost a memory round trip per row (2.6 us of a 4.8 us launch
+// for one token of 8 heads). Index arithmetic is 32-bit (the host takes this
+// path only when rows * D / 8 < 2^32).
+// Rows per thread of the vector quantize / dequantize kernels: four for
+// large launches (more loads in flight per lane), one for launches of at
+// most kSmallChunks 8-element chunks. A small launch (a decode token's K or
+// V) runs one or a few waves whose time is their instruction latency: for
+// one token of 8 heads, four rows per lane took 4.5 us and one row 2.2 us.
+constexpr int kQuantRows = 4;
+constexpr int64_t kSmallChunks = 256 * 1024;
 
 template <int XDT, int LPG, int RPT>  // LPG = lanes per group = G / 8
 __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
@@ -141,9 +151,10 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
   const uint32_t ch = slot ? idx - r0 * cpr : 0u;
   const uint32_t S = (uint32_t)a.S, H = (uint32_t)a.H;
 
-  float x[RPT][8];
+  constexpr int NW = XDT == KVQ_F32 ? 2 : 1;  // 16-byte loads per chunk
   bool live[RPT];
   uint32_t bb[RPT], hh[RPT], ss[RPT];
+  uint4 raw[RPT][NW];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
     const uint32_t row = r0 + (uint32_t)k * rq;
@@ -154,14 +165,33 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     hh[k] = bh % H;
     bb[k] = bh / H;
     const int64_t xoff = (int64_t)bb[k] * a.xs_b + (int64_t)hh[k] * a.xs_h + (int64_t)ss[k] * a.xs_s + 8 * ch;
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+      raw[k][n] = *(const uint4*)((const uint8_t*)a.x + (xoff + 4 * n) * (NW * 2));
+  }
+  int64_t pos[RPT];
+  if (a.write_pos) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) pos[k] = (int64_t)a.write_pos[bb[k]] + ss[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) pos[k] = a.write_pos0 + ss[k];
+  }
+  int64_t dst[RPT];  // destination row; < 0: paged, no block holds it
+  page_rows<RPT>(a.pm, bb, pos, dst);
+  float x[RPT][8];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
     if constexpr (XDT == KVQ_F32) {
-      const float4 lo = *(const float4*)((const float*)a.x + xoff);
-      const float4 hi = *(const float4*)((const float*)a.x + xoff + 4);
-      x[k][0] = lo.x; x[k][1] = lo.y; x[k][2] = lo.z; x[k][3] = lo.w;
-      x[k][4] = hi.x; x[k][5] = hi.y; x[k][6] = hi.z; x[k][7] = hi.w;
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        x[k][4 * n + 0] = __builtin_bit_cast(float, raw[k][n].x);
+        x[k][4 * n + 1] = __builtin_bit_cast(float, raw[k][n].y);
+        x[k][4 * n + 2] = __builtin_bit_cast(float, raw[k][n].z);
+        x[k][4 * n + 3] = __builtin_bit_cast(float, raw[k][n].w);
+      }
     } else {
-      const uint4 w = *(const uint4*)((const uint16_t*)a.x + xoff);
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t wd[4] = {raw[k][0].x, raw[k][0].y, raw[k][0].z, raw[k][0].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if constexpr (XDT == KVQ_BF16) {
@@ -196,8 +226,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
       qf = fminf(fmaxf(qf, -8.0f), 7.0f);
       word |= (uint32_t)((int)qf + 8) << (4 * e);
     }
-    const int64_t b = bb[k], h = hh[k];
-    const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + ss[k]);
+    const int64_t b = bb[k], h = hh[k], pos = dst[k];
     if (pos < 0) continue;  // paged: no block holds this position
     // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
     *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
@@ -217,7 +246,7 @@ struct DequantArgs {
   void* out;
   int64_t os_b, os_h, os_s, os_d;
   int scale_dtype, out_dtype;
-  PageMap pm;  // pm.table != nullptr: packed/scales are pools (ps_b = ss_b = 0)
+  PageMap pm;  // pm.paged: packed/scales are pools (ps_b = ss_b = 0)
 };
 
 __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
@@ -231,7 +260,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
   const int64_t b = bh / a.H;
 
   const int64_t obase = b * a.os_b + h * a.os_h + s * a.os_s;
-  const int64_t r = a.pm.table ? page_row(a.pm, b, s) : s;
+  const int64_t r = a.pm.paged ? page_row(a.pm, b, s) : s;
   if (r < 0) {  // paged: no block holds this position -> zeros
     for (int64_t c = g * a.G; c < (g + 1) * a.G && c < a.d_out; ++c)
       store_from_f32(a.out, obase + c * a.os_d, a.out_dtype, 0.0f);
@@ -266,7 +295,8 @@ __global__ __launch_bounds__(256) void dequantize_vec_kernel(const DequantArgs a
   const uint32_t S = (uint32_t)a.S, H = (uint32_t)a.H;
   uint32_t w[RPT];
   float sc[RPT];
-  int64_t obase[RPT];
+  int64_t obase[RPT], pos[RPT], r[RPT];
+  uint32_t bb[RPT], hh[RPT];
   bool live[RPT];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
@@ -274,15 +304,30 @@ __global__ __launch_bounds__(256) void dequantize_vec_kernel(const DequantArgs a
     live[k] = row < rows;
     const uint32_t rw = live[k] ? row : 0u;
     const uint32_t s = rw % S, bh = rw / S;
-    const int64_t h = bh % H, b = bh / H;
-    obase[k] = b * a.os_b + h * a.os_h + (int64_t)s * a.os_s + 8 * ch;
-    const int64_t r = a.pm.table ? page_row(a.pm, b, s) : (int64_t)s;
-    if (r < 0) {  // paged: no block holds this position -> zeros
+    hh[k] = bh % H;
+    bb[k] = bh / H;
+    pos[k] = s;
+    obase[k] = (int64_t)bb[k] * a.os_b + (int64_t)hh[k] * a.os_h + (int64_t)s * a.os_s + 8 * ch;
+  }
+  // All table reads in flight together, then all code and scale reads. An
+  // absent position reads pool row 0 (present whenever the pool has a block)
+  // and has its result replaced by zeros.
+  page_rows<RPT>(a.pm, bb, pos, r);
+  if (!a.pm.paged || a.pm.n_blocks > 0) {
+    int64_t si[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int64_t b = bb[k], h = hh[k], rr = r[k] < 0 ? 0 : r[k];
+      w[k] = *(const uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + rr * a.ps_s + 4 * ch);
+      si[k] = b * a.ss_b + h * a.ss_h + rr * a.ss_s + (8 * ch) / a.G;
+    }
+    load_n_as_f32<RPT>(a.scales, si, a.scale_dtype, sc);
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    if (r[k] < 0) {  // paged: no block holds this position -> zeros
       w[k] = 0x88888888u;
       sc[k] = 0.0f;
-    } else {
-      w[k] = *(const uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + r * a.ps_s + 4 * ch);
-      sc[k] = load_as_f32(a.scales, b * a.ss_b + h * a.ss_h + r * a.ss_s + (8 * ch) / a.G, a.scale_dtype);
     }
   }
 #pragma unroll
@@ -322,6 +367,22 @@ using namespace kvq;
 
 namespace {
 
+template <int XDT, int RPT>
+void launch_qvec(int lpg, dim3 grid, hipStream_t st, const QuantArgs& a) {
+  switch (lpg) {
+    case 1: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 1, RPT>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 2, RPT>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 4, RPT>), grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 8, RPT>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 16, RPT>), grid, dim3(256), 0, st, a); break;
+  }
+}
+
+template <int ODT, int RPT>
+void launch_dqvec(dim3 grid, hipStream_t st, const DequantArgs& a) {
+  hipLaunchKernelGGL((dequantize_vec_kernel<ODT, RPT>), grid, dim3(256), 0, st, a);
+}
+
 // Checks a paged-pool description shared by the paged entry points and
 // fills `pm`. Pools are [H, num_blocks << page_shift, ...]; the entry point's
 // stride arrays give (head, row) strides and the batch stride is 0.
@@ -336,6 +397,7 @@ int page_map(const char* who, const int32_t* block_table, int64_t table_stride, 
   KVQ_CHECK_ARG(num_blocks <= (int64_t(1) << 31) / page_size, "%s: pool too large", who);
   int shift = 0;
   while ((int64_t(1) << shift) < page_size) ++shift;
+  pm->paged = 1;
   pm->table = block_table;
   pm->tab_stride = table_stride;
   pm->n_pages = table_cols;
@@ -386,22 +448,15 @@ int quantize_impl(const char* who, const void* x, int x_dtype, const int64_t* x_
                    (uintptr_t)packed % 4 == 0 && a.ps_b % 4 == 0 && a.ps_h % 4 == 0 && a.ps_s % 4 == 0 &&
                    rows * (D / 8) < (1ll << 32) - 256 * kQuantRows;
   if (vec) {
-    const int64_t total = (rows + kQuantRows - 1) / kQuantRows * (D / 8);
+    const bool small = rows * (D / 8) <= kSmallChunks;
+    const int rpt = small ? 1 : kQuantRows;
+    const int64_t total = (rows + rpt - 1) / rpt * (D / 8);
     const dim3 grid((unsigned)((total + 255) / 256));
-#define KVQ_QVEC(XDT)                                                                                          \
-    switch (lpg) {                                                                                             \
-      case 1: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 1, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
-      case 2: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 2, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
-      case 4: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 4, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
-      case 8: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 8, kQuantRows>), grid, dim3(256), 0, st, a); break;   \
-      default: hipLaunchKernelGGL((quantize_vec_kernel<XDT, 16, kQuantRows>), grid, dim3(256), 0, st, a); break; \
-    }
     switch (x_dtype) {
-      case KVQ_BF16: KVQ_QVEC(KVQ_BF16) break;
-      case KVQ_F16: KVQ_QVEC(KVQ_F16) break;
-      default: KVQ_QVEC(KVQ_F32) break;
+      case KVQ_BF16: small ? launch_qvec<KVQ_BF16, 1>(lpg, grid, st, a) : launch_qvec<KVQ_BF16, kQuantRows>(lpg, grid, st, a); break;
+      case KVQ_F16: small ? launch_qvec<KVQ_F16, 1>(lpg, grid, st, a) : launch_qvec<KVQ_F16, kQuantRows>(lpg, grid, st, a); break;
+      default: small ? launch_qvec<KVQ_F32, 1>(lpg, grid, st, a) : launch_qvec<KVQ_F32, kQuantRows>(lpg, grid, st, a); break;
     }
-#undef KVQ_QVEC
     KVQ_CHECK_LAUNCH(who);
     return KVQ_OK;
   }
@@ -453,12 +508,14 @@ int dequantize_impl(const void* packed, const int64_t* packed_strides,
                    a.ps_h % 4 == 0 && a.ps_s % 4 == 0 && rows * (d_out / 8) < (1ll << 32) - 256 * kQuantRows;
   hipStream_t st = (hipStream_t)stream;
   if (vec) {
-    const int64_t total = (rows + kQuantRows - 1) / kQuantRows * (d_out / 8);
+    const bool small = rows * (d_out / 8) <= kSmallChunks;
+    const int rpt = small ? 1 : kQuantRows;
+    const int64_t total = (rows + rpt - 1) / rpt * (d_out / 8);
     const dim3 grid((unsigned)((total + 255) / 256));
     switch (out_dtype) {
-      case KVQ_BF16: hipLaunchKernelGGL((dequantize_vec_kernel<KVQ_BF16, kQuantRows>), grid, dim3(256), 0, st, a); break;
-      case KVQ_F16: hipLaunchKernelGGL((dequantize_vec_kernel<KVQ_F16, kQuantRows>), grid, dim3(256), 0, st, a); break;
-      default: hipLaunchKernelGGL((dequantize_vec_kernel<KVQ_F32, kQuantRows>), grid, dim3(256), 0, st, a); break;
+      case KVQ_BF16: small ? launch_dqvec<KVQ_BF16, 1>(grid, st, a) : launch_dqvec<KVQ_BF16, kQuantRows>(grid, st, a); break;
+      case KVQ_F16: small ? launch_dqvec<KVQ_F16, 1>(grid, st, a) : launch_dqvec<KVQ_F16, kQuantRows>(grid, st, a); break;
+      default: small ? launch_dqvec<KVQ_F32, 1>(grid, st, a) : launch_dqvec<KVQ_F32, kQuantRows>(grid, st, a); break;
     }
     KVQ_CHECK_LAUNCH("kvq_dequantize");
     return KVQ_OK;
@@ -478,7 +535,7 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
                             const int32_t* write_pos, int64_t write_pos0,
                             void* stream) {
   clear_error();
-  const PageMap pm{nullptr, 0, 0, 0, 0};
+  const PageMap pm{0, nullptr, 0, 0, 0, 0};
   return quantize_impl("kvq_quantize", x, x_dtype, x_strides, B, H, S, D, group_size, packed,
                        packed_strides, scales, scale_dtype, scale_strides, write_pos, write_pos0, pm,
                        stream);
@@ -510,7 +567,7 @@ extern "C" int kvq_dequantize(const void* packed, const int64_t* packed_strides,
                               void* out, int out_dtype, const int64_t* out_strides, int64_t d_out,
                               void* stream) {
   clear_error();
-  const PageMap pm{nullptr, 0, 0, 0, 0};
+  const PageMap pm{0, nullptr, 0, 0, 0, 0};
   return dequantize_impl(packed, packed_strides, scales, scale_dtype, scale_strides, B, H, S,
                          group_size, num_groups, out, out_dtype, out_strides, d_out, pm, stream);
 }

@@ -126,6 +126,52 @@ def test_dequantize_paged_matches_contiguous():
         assert torch.all(out[b, :, cap:] == 0)
 
 
+def test_quantize_dequantize_paged_large_launch():
+    """Launches above 256K 8-element chunks take four rows per lane: codes
+    through the table against the oracle, dequantize_paged against the
+    contiguous dequantize of the gathered rows."""
+    B, H, S, D, G, P = 3, 8, 1400, 128, 32, 64
+    lens = [1400, 1100, 333]
+    assert B * H * S * D // 8 > 256 * 1024
+    n_blocks = sum(-(-n // P) for n in lens) + 3
+    table = _table(lens, P, n_blocks, seed=41)
+    pt = ops.PageTable(table, P, n_blocks)
+    pools = _pools(H, n_blocks, P, D, G, torch.bfloat16)
+    x = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(41)).to(torch.bfloat16)
+    ops.quantize_into_paged(x.to(DEV), pools[0], pools[1], pt, G, 0)
+    want_p, want_s = O.quantize_int4(x.float().numpy(), G, "bf16")
+    got_p = _gather(pools[0], table, P, S).cpu().numpy()
+    got_s = _gather(pools[1], table, P, S).float().cpu().numpy()
+    for b, n in enumerate(lens):
+        assert np.array_equal(got_p[b, :, :n], want_p[b, :, :n]), b
+        assert np.array_equal(O.bits(got_s[b, :, :n], "bf16"), O.bits(want_s[b, :, :n], "bf16")), b
+    out = ops.dequantize_paged(pools[0], pools[1], pt, B, S, G, D, torch.bfloat16)
+    want = ops.dequantize(_gather(pools[0], table, P, S).contiguous(), _gather(pools[1], table, P, S).contiguous(),
+                          G, D, torch.bfloat16)
+    for b, n in enumerate(lens):
+        cap = -(-n // P) * P
+        assert torch.equal(out[b, :, :cap], want[b, :, :cap]), b
+        assert torch.all(out[b, :, cap:] == 0), b
+
+
+@pytest.mark.parametrize("S", [20, 1100])
+def test_table_without_columns_maps_nothing(S):
+    """A block table with no columns places no position: the quantizer writes
+    nothing and the dequantizer returns zeros (at one and four rows per lane)."""
+    B, H, D, G, P, n_blocks = 2, 8, 128, 32, 16, 4
+    table = torch.empty((B, 0), dtype=torch.int32, device=DEV)
+    pt = ops.PageTable(table, P, n_blocks)
+    pools = _pools(H, n_blocks, P, D, G, torch.bfloat16)
+    before = [t.clone() for t in pools]
+    x = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(S)).to(torch.bfloat16)
+    ops.quantize_into_paged(x.to(DEV), pools[0], pools[1], pt, G, 0)
+    torch.cuda.synchronize()
+    for now, was in zip(pools, before):
+        assert torch.equal(now, was)
+    out = ops.dequantize_paged(pools[0], pools[1], pt, B, S, G, D, torch.bfloat16)
+    assert out.shape == (B, H, S, D) and torch.all(out == 0)
+
+
 ATTN_CASES = [
     # B, Hq, Hkv, D, G, page, lens, dtype
     (1, 32, 8, 128, 32, 64, [16385], "bf16"),
