@@ -232,6 +232,68 @@ class QuantizedKVCacheBase:
         v = ops.dequantize(vp, vs, self.group_size, d_head, out_dtype)
         return k, v
 
+    # -- batch and length edits (generate(): beam search, assisted decoding) --
+    def _gather_batch(self, index: torch.Tensor) -> None:
+        """Every layer keeps the batch rows `index` (int64), in that order:
+        new sequence b is old sequence index[b]. Each layer's stored rows are
+        copied into fresh capacity buffers."""
+        for layer in self._layers.values():
+            n = layer.seq_len
+            idx = index.to(layer.k_packed.device)
+            bufs = []
+            for t in (layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales):
+                new = torch.empty((idx.numel(),) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
+                new[:, :, :n] = t[idx, :, :n]
+                bufs.append(new)
+            layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales = bufs
+            if layer.seq_lens is not None:
+                layer.seq_lens = layer.seq_lens[idx].contiguous()
+
+    def _batch_size(self) -> int:
+        return int(next(iter(self._layers.values())).k_packed.shape[0]) if self._layers else 0
+
+    def reorder_cache(self, beam_idx: torch.Tensor) -> None:
+        """Beam search (HF ``Cache.reorder_cache``): sequence b becomes the old
+        sequence beam_idx[b]."""
+        self._gather_batch(beam_idx.long())
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        """Keep only the batch rows `indices` (int indices or a bool mask)."""
+        idx = indices.nonzero().flatten() if indices.dtype == torch.bool else indices.long()
+        self._gather_batch(idx)
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        """Repeat every sequence `repeats` times along the batch."""
+        self._gather_batch(torch.arange(self._batch_size()).repeat_interleave(int(repeats)))
+
+    def activate_past_recording(self) -> None:
+        """HF assisted decoding calls this before drafting. Every stored token
+        is kept until ``crop``, so there is nothing to switch on."""
+
+    def get_max_length(self, layer_idx: int = 0) -> int:
+        """transformers 5.15 name of ``get_max_cache_shape``: -1, no maximum."""
+        return -1
+
+    def crop(self, max_length: int) -> None:
+        """Drop tokens from the end of every layer (HF ``Cache.crop``):
+        max_length < 0 removes -max_length tokens; max_length > 0 keeps the
+        first max_length (nothing if that is not shorter); 0 does nothing. A
+        ragged layer cuts every sequence by the same rule."""
+        max_length = int(max_length)
+        if max_length == 0:
+            return
+        for layer in self._layers.values():
+            n = layer.seq_len
+            keep = max(n + max_length, 0) if max_length < 0 else min(max_length, n)
+            if keep == n:
+                continue
+            if layer.seq_lens is not None:
+                if max_length < 0:
+                    layer.seq_lens.add_(max_length).clamp_(min=0)
+                else:
+                    layer.seq_lens.clamp_(max=keep)
+            layer.seq_len = keep
+
     def nbytes(self) -> int:
         """Bytes of packed codes + scales for the stored tokens of all layers
         (same accounting as the reference, models/llama3/kv_cache.py:158-166)."""

@@ -14,6 +14,13 @@ names the same positions in each layer's pool. Blocks are taken from a free
 list as sequences grow; the pools grow by doubling (block ids stay valid), and
 ``free_sequence`` returns a finished sequence's blocks for reuse by another.
 
+Blocks are reference-counted so that sequences can share them: beam search's
+``reorder_cache`` (and ``batch_select_indices`` / ``batch_repeat_interleave``)
+hands a parent's blocks to each of its children without copying, and the
+first write into a shared block copies that one block (every layer's rows)
+to a fresh one (copy on write). ``crop`` shortens sequences for assisted
+decoding and releases blocks past the new ends.
+
 Every sequence has its own length (ragged batches are the normal case). The
 HIP kernels read and write through the table: ``quantize_into_paged`` for
 appends, ``decode_step_paged`` for a decode token (append + attention in one
@@ -62,6 +69,7 @@ class PagedQuantizedKVCache:
         self._seq_lens: dict[int, torch.Tensor] = {}    # device int32 [B] per layer
         self._pages: list[list[int]] = []               # block ids of each sequence
         self._free: list[int] = []
+        self._ref: list[int] = []                       # sequences holding each block
         self._num_blocks = 0
         self._table: Optional[torch.Tensor] = None
         self._table_dirty = False
@@ -97,7 +105,42 @@ class PagedQuantizedKVCache:
                 dst[:, :old_rows].copy_(src[:, :old_rows])
             self._pools[idx] = new
         self._free.extend(range(n_blocks - 1, self._num_blocks - 1, -1))
+        self._ref.extend([0] * (n_blocks - self._num_blocks))
         self._num_blocks = n_blocks
+
+    def _take_block(self) -> int:
+        if not self._free:
+            self._grow_pool(max(2 * self._num_blocks, 8))
+        blk = self._free.pop()
+        self._ref[blk] = 1
+        return blk
+
+    def _release(self, blk: int) -> None:
+        self._ref[blk] -= 1
+        if self._ref[blk] == 0:
+            self._free.append(blk)
+
+    def _make_writable(self, starts: list[int], n_new: int | list[int]) -> None:
+        """Before sequence b writes positions [starts[b], starts[b] + n), give
+        it its own copy of every shared block those positions fall in."""
+        P = self.page_size
+        for b, lo in enumerate(starts):
+            n = n_new[b] if isinstance(n_new, list) else n_new
+            if n <= 0:
+                continue
+            pages = self._pages[b]
+            for i in range(lo // P, min((lo + n - 1) // P + 1, len(pages))):
+                old = pages[i]
+                if self._ref[old] <= 1:
+                    continue
+                new = self._take_block()
+                src, dst = slice(old * P, (old + 1) * P), slice(new * P, (new + 1) * P)
+                for pools in self._pools.values():
+                    for t in pools:
+                        t[:, dst] = t[:, src]
+                self._release(old)
+                pages[i] = new
+                self._table_dirty = True
 
     def _ensure_pages(self, lengths: list[int]) -> None:
         """Give every sequence blocks for its first lengths[b] positions."""
@@ -107,7 +150,7 @@ class PagedQuantizedKVCache:
             self._grow_pool(max(2 * self._num_blocks, self._num_blocks + short, 8))
         for b, n in enumerate(need):
             for _ in range(n):
-                self._pages[b].append(self._free.pop())
+                self._pages[b].append(self._take_block())
                 self._table_dirty = True
         cols = max((len(p) for p in self._pages), default=0)
         if self._table is None or self._table.shape[1] < cols:
@@ -142,7 +185,8 @@ class PagedQuantizedKVCache:
     def free_sequence(self, b: int) -> None:
         """Return sequence b's blocks to the free list and zero its length in
         every layer (the slot can then take a new sequence)."""
-        self._free.extend(reversed(self._pages[b]))
+        for blk in reversed(self._pages[b]):
+            self._release(blk)
         self._pages[b] = []
         self._table_dirty = True
         for idx in self._lens:
@@ -164,6 +208,7 @@ class PagedQuantizedKVCache:
             raise ValueError(f"layer {layer_idx} already holds state")
         self._layer(layer_idx)
         self._ensure_pages(lens)
+        self._make_writable([0] * B, list(lens))
         pools = self._pools[layer_idx]
         pt = self._page_table()
         t = torch.arange(S, device=kp.device)
@@ -186,6 +231,7 @@ class PagedQuantizedKVCache:
         S = int(key_states.shape[2])
         lens = self._lens[layer_idx]
         self._ensure_pages([n + S for n in lens])
+        self._make_writable(lens, S)
         pools = self._pools[layer_idx]
         pt = self._page_table()
         pos = self._seq_lens[layer_idx]
@@ -208,6 +254,7 @@ class PagedQuantizedKVCache:
         if any(n < 0 or n > key_states.shape[2] for n in lens):
             raise ValueError("lengths must lie in [0, S_max]")
         self._ensure_pages(lens)
+        self._make_writable([0] * len(lens), int(key_states.shape[2]))
         pools = self._pools[layer_idx]
         pt = self._page_table()
         # rows past a sequence's length land in its last page's slack or, past
@@ -232,6 +279,7 @@ class PagedQuantizedKVCache:
         self._setup(key_states)
         lens = self._lens[layer_idx]
         self._ensure_pages([n + 1 for n in lens])
+        self._make_writable(lens, 1)
         pools = self._pools[layer_idx]
         pt = self._page_table()
         pos = self._seq_lens[layer_idx]
@@ -270,6 +318,72 @@ class PagedQuantizedKVCache:
         uniform = all(n == S for n in lens)
         return ops.dense_attention(query_states, k, v, n_kv_heads=n_kv_heads, is_causal=is_causal,
                                    sm_scale=scale, seq_lens=None if uniform else seq_lens)
+
+    # -- batch and length edits (generate(): beam search, assisted decoding) --
+    def _remap(self, src: list[int]) -> None:
+        """New sequence b continues old sequence src[b] (sharing its blocks)."""
+        if self._shape is None:
+            return
+        B = self._shape[0]
+        if any(s < 0 or s >= B for s in src):
+            raise IndexError(f"batch index out of range for a batch of {B}")
+        new_pages = [list(self._pages[s]) for s in src]
+        for pages in new_pages:
+            for blk in pages:
+                self._ref[blk] += 1
+        for pages in self._pages:
+            for blk in pages:
+                self._release(blk)
+        self._pages = new_pages
+        self._shape = (len(src),) + self._shape[1:]
+        index = torch.tensor(src, dtype=torch.int64, device=self._shape[5])
+        for idx in self._lens:
+            self._lens[idx] = [self._lens[idx][s] for s in src]
+            self._seq_lens[idx] = self._seq_lens[idx][index].contiguous()
+        self._table = None
+        self._table_dirty = True
+
+    def reorder_cache(self, beam_idx: torch.Tensor) -> None:
+        """Beam search (HF ``Cache.reorder_cache``): sequence b becomes the old
+        sequence beam_idx[b]."""
+        self._remap([int(i) for i in beam_idx.tolist()])
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        """Keep only the batch rows `indices` (int indices or a bool mask)."""
+        idx = indices.nonzero().flatten() if indices.dtype == torch.bool else indices
+        self._remap([int(i) for i in idx.tolist()])
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        """Repeat every sequence `repeats` times along the batch."""
+        if self._shape is not None:
+            self._remap([b for b in range(self._shape[0]) for _ in range(int(repeats))])
+
+    def activate_past_recording(self) -> None:
+        """HF assisted decoding calls this before drafting. Every stored token
+        is kept until ``crop``, so there is nothing to switch on."""
+
+    def get_max_length(self, layer_idx: int = 0) -> int:
+        """transformers 5.15 name of ``get_max_cache_shape``: -1, no maximum."""
+        return -1
+
+    def crop(self, max_length: int) -> None:
+        """Drop tokens from the end of every sequence of every layer (HF
+        ``Cache.crop``): max_length < 0 removes -max_length tokens;
+        max_length > 0 keeps at most the first max_length; 0 does nothing.
+        Blocks past every layer's new end are released."""
+        max_length = int(max_length)
+        if max_length == 0 or self._shape is None:
+            return
+        for idx, lens in self._lens.items():
+            new = [max(n + max_length, 0) if max_length < 0 else min(n, max_length) for n in lens]
+            self._lens[idx] = new
+            self._seq_lens[idx].copy_(torch.tensor(new, dtype=torch.int32))
+        P = self.page_size
+        for b, pages in enumerate(self._pages):
+            keep = -(-max((lens[b] for lens in self._lens.values()), default=0) // P)
+            while len(pages) > keep:
+                self._release(pages.pop())
+                self._table_dirty = True
 
     # -- views ---------------------------------------------------------------
     def block_table(self) -> torch.Tensor:
