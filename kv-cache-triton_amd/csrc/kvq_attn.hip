@@ -628,9 +628,10 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vp_bh, Le * vps);
   const __amdgpu_buffer_rsrc_t rvs = buffer_rsrc(vs_bh, Le * vss2);
   // Paged tiles: a 64-key tile starting at t0 (a multiple of 64) lies in one
-  // page, so its keys are rows t0 + delta + j for j < lim (lim = the keys it
-  // has before t_end, 0 if no block holds the page); key j >= lim is given the
-  // pool's end as offset and reads zero.
+  // page, so its keys are pool rows rb + j for j < lim (lim = the keys it has
+  // before t_end, 0 if no block holds the page). Its loads go through buffers
+  // that start at row rb and hold lim rows: key j >= lim falls outside them
+  // and reads zero, with no per-load offset select.
   // The block of each of this wave's tiles (tiles wave, wave + NW, ... of
   // the split; lane k holds tile k's), read from the table once here so that
   // a refill's loads wait for no table read. The first CH tiles (loaded at
@@ -652,10 +653,11 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
       const uint32_t k = (((t0 - (uint32_t)t_begin) >> 6) - (uint32_t)wave) / (uint32_t)NW;  // wave-uniform
       int32_t blk;
       if (k >= (uint32_t)CH && k < 64u) blk = __builtin_amdgcn_readlane(wave_blk, (int)k);
-      else blk = pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1;
-      const bool ok = blk >= 0 && blk < a.n_blocks;
-      rb = t0 + (((uint32_t)blk - pg) << a.page_shift);
-      lim = (ok && t0 < (uint32_t)t_end) ? min(64u, (uint32_t)t_end - t0) : 0u;
+      else blk = __builtin_amdgcn_readfirstlane(pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1);
+      const bool ok = blk >= 0 && blk < a.n_blocks && t0 < (uint32_t)t_end;
+      // wave-uniform; readfirstlane keeps the tile's buffers in scalar registers
+      rb = __builtin_amdgcn_readfirstlane(ok ? t0 + (((uint32_t)blk - pg) << a.page_shift) : 0u);
+      lim = __builtin_amdgcn_readfirstlane(ok ? min(64u, (uint32_t)t_end - t0) : 0u);
     }
   };
   const int ng = (D + a.G - 1) / a.G;  // scales per token row: 1, 2 or 4 (wave-uniform)
@@ -691,25 +693,36 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArg
   auto load_k = [&](int i, int base) {
     uint32_t rb, lim;
     tile_rows(tile_t0(i, base), rb, lim);
-    const uint32_t r = rb + lane;
-    const bool in = !PAGED || (uint32_t)lane < lim;
+    __amdgpu_buffer_rsrc_t tk = rk, tks = rks;
+    uint32_t r0 = rb;
+    if constexpr (PAGED) {
+      tk = buffer_rsrc(kp_bh + (size_t)rb * kps, lim * kps);
+      tks = buffer_rsrc((const uint8_t*)ks_bh + (size_t)rb * kss2, lim * kss2);
+      r0 = 0;
+    }
+    const uint32_t r = r0 + lane;
 #pragma unroll
     for (int c = 0; c < LPT; ++c)
-      kc4[i][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rk, in ? r * kps + 16u * c : Le * kps, 0, 0));
-    skr[i] = load_scales(rks, in ? r * kss2 : Le * kss2);
+      kc4[i][c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(tk, r * kps + 16u * c, 0, 0));
+    skr[i] = load_scales(tks, r * kss2);
   };
   auto load_v = [&](int i, int base) {
     uint32_t rb, lim;
     tile_rows(tile_t0(i, base), rb, lim);
-    svr[i] = load_scales(rvs, (!PAGED || (uint32_t)lane < lim) ? (rb + lane) * vss2 : Le * vss2);
+    __amdgpu_buffer_rsrc_t tv = rv, tvs = rvs;
+    uint32_t r0 = rb;
+    if constexpr (PAGED) {
+      tv = buffer_rsrc(vp_bh + (size_t)rb * vps, lim * vps);
+      tvs = buffer_rsrc((const uint8_t*)vs_bh + (size_t)rb * vss2, lim * vss2);
+      r0 = 0;
+    }
+    svr[i] = load_scales(tvs, (r0 + lane) * vss2);
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const uint32_t j = (uint32_t)(s * SUB + VTS * k + vts);
-        vq[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(
-            rv, (!PAGED || j < lim) ? (rb + j) * vps + 4u * (uint32_t)vj : Le * vps, 0, 0);
+        vq[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(tv, (r0 + j) * vps + 4u * (uint32_t)vj, 0, 0);
       }
   };
 
