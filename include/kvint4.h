@@ -101,7 +101,8 @@ int kvq_dequantize(const void* packed, const int64_t* packed_strides,
  * shape on a device with `num_cus` compute units (>= 1), or a negative status.
  * `s_max` is the longest sequence (tokens) that will be attended. bf16/fp16
  * queries with 16-bit scales run on the matrix-core kernel, other dtype pairs
- * on the exact-fp32 VALU kernel; the plan depends on which.
+ * on the exact-fp32 VALU kernel; the plan depends on which. An empty batch
+ * (B == 0 or Sq == 0) plans 1 split and needs no workspace.
  */
 int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
                                    int64_t D, int64_t s_max, int q_dtype, int scale_dtype,

@@ -1651,6 +1651,7 @@ extern "C" int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv
     set_error("kvq_decode_attn_num_splits: q and scale dtypes must be bf16/fp16/fp32");
     return KVQ_EINVAL;
   }
+  if ((B == 0 || Sq == 0) && B >= 0 && Sq >= 0) return 1;  // nothing to launch
   Plan p;
   const int rc = make_plan(B, Hq, Hkv, Sq, D, s_max, q_dtype, scale_dtype, 0, num_cus, &p);
   if (rc != KVQ_OK) {
@@ -1670,6 +1671,7 @@ extern "C" int64_t kvq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_
     set_error("kvq_decode_attn_workspace_bytes: bad dtype or n_split");
     return KVQ_EINVAL;
   }
+  if ((B == 0 || Sq == 0) && B >= 0 && Sq >= 0) return 0;  // nothing to launch
   // s_max only bounds n_split in planning; pass one long enough that every
   // split reaches min_split_tokens, so the plan keeps n_split.
   Plan p;

@@ -52,6 +52,11 @@ def test_num_splits_planning():
     assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 16384, F32, F16, 256) == 16
     assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 96, 1024, B16, B16, 256) == nat.KVQ_EUNSUP
     assert lib.kvq_decode_attn_num_splits(1, 30, 8, 1, 128, 1024, B16, B16, 256) == nat.KVQ_EINVAL
+    # an empty batch or query block launches nothing: one split, no workspace
+    assert lib.kvq_decode_attn_num_splits(0, 32, 8, 1, 128, 1024, B16, B16, 256) == 1
+    assert lib.kvq_decode_attn_num_splits(2, 32, 8, 0, 128, 1024, B16, B16, 256) == 1
+    assert lib.kvq_decode_attn_workspace_bytes(0, 32, 8, 1, 128, B16, B16, 1) == 0
+    assert lib.kvq_decode_attn_num_splits(-1, 32, 8, 1, 128, 1024, B16, B16, 256) == nat.KVQ_EINVAL
 
 
 def test_workspace_bytes():
