@@ -530,8 +530,15 @@ __device__ __forceinline__ void chunk_scales(uint2 raw, bool g32, const uint32_t
   }
 }
 
+// D = 64 with one row set fits 128 VGPRs: four waves per SIMD, so two
+// 8-wave workgroups share a CU (a batch of many short sequences then runs
+// in one round of workgroups instead of two).
+template <int D, int RS>
+constexpr int mfma_waves_per_simd() { return D == 64 && RS == 1 ? 4 : 1; }
+
 template <int D, int RS, int QM, int SM, bool ROWMASK, int NW, int CH, bool PAGED>
-__global__ __launch_bounds__(64 * NW) void decode_attn_mfma_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mfma_waves_per_simd<D, RS>())))
+void decode_attn_mfma_kernel(const AttnArgs a) {
   constexpr bool F16 = QM == KVQ_F16;
   constexpr bool S_F16 = SM == KVQ_F16;
   constexpr int LPT = D / 32;       // 32-dim chunks (16 code bytes) per token
