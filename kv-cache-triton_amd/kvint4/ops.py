@@ -22,9 +22,20 @@ from . import _native as nat
 
 SUPPORTED_FLOATS = (torch.bfloat16, torch.float16, torch.float32)
 
-# Query rows (GQA group x query length) above which a multi-token query is
-# routed to dequantize + dense SDPA instead of the decode kernel.
-MAX_FUSED_ROWS = 64
+# Query rows per KV head (GQA group x query length) above which a multi-token
+# query block goes to dequantize + dense SDPA instead of the fused kernel. The
+# fused kernel streams the cache once per 8 rows; on one MI355X it is the
+# faster route up to 1024 rows and flash SDPA beyond 2048, at 512 to 16K keys
+# (e.g. 16K keys, GQA 4: 256 queries 610 vs 652 us, 512 queries 1251 vs 654 us).
+MAX_FUSED_ROWS = 1024
+
+
+def dense_fast_path(q: torch.Tensor, seq_lens: torch.Tensor | None) -> bool:
+    """Whether dense_attention runs the fused flash SDPA kernel for this query
+    (16-bit queries, one length for the whole batch); otherwise it masks
+    explicitly on the fp32 math backend, and the fused kernel is preferred at
+    any block length."""
+    return q.dtype in (torch.bfloat16, torch.float16) and seq_lens is None
 
 
 def packed_width(d: int, group_size: int) -> int:
@@ -428,6 +439,18 @@ def dense_attention(
     B, Hq, Sq, D = q.shape
     Sk = k.shape[2]
     ratio = Hq // n_kv_heads
+    if dense_fast_path(q, seq_lens) and is_causal and 0 < Sq < Sk:
+        # bottom-right causal block (a prompt chunk after cached tokens): the
+        # flash kernel with its lower-right causal variant and native GQA
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        from torch.nn.attention.bias import causal_lower_right
+
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                return F.scaled_dot_product_attention(q, k, v, attn_mask=causal_lower_right(Sq, Sk),
+                                                      scale=sm_scale, enable_gqa=True)
+        except RuntimeError:
+            pass
     if (ratio > 1 and seq_lens is None and not (is_causal and Sq != Sk)
             and q.dtype in (torch.bfloat16, torch.float16)):
         # the fused SDPA kernels read each KV head for its whole query group
@@ -481,7 +504,7 @@ def attention_over_quantized(
     B, Hq, Sq, D = q.shape
     Sk = k_packed.shape[2]
     rows = (Hq // n_kv_heads) * Sq
-    use_fused = rows <= MAX_FUSED_ROWS or (is_causal and Sq != Sk)
+    use_fused = rows <= MAX_FUSED_ROWS or (is_causal and Sq != Sk and not dense_fast_path(q, seq_lens))
     if use_fused:
         try:
             return fused_decode_attention(

@@ -305,17 +305,18 @@ class PagedQuantizedKVCache:
         B, Hq, Sq, D = query_states.shape
         lens = self._lens[layer_idx]
         rows = (Hq // n_kv_heads) * Sq
-        if self.page_size >= 64 and rows <= ops.MAX_FUSED_ROWS:
+        S = max(lens, default=0)
+        uniform = all(n == S for n in lens)
+        dense_fast = ops.dense_fast_path(query_states, None if uniform else seq_lens)
+        if self.page_size >= 64 and (rows <= ops.MAX_FUSED_ROWS or not dense_fast):
             try:
                 return ops.fused_decode_attention_paged(
                     query_states, *pools, pt, n_kv_heads=n_kv_heads, group_size=self.group_size,
                     is_causal=is_causal, sm_scale=scale, seq_lens=seq_lens)
             except _native.KVQUnsupported:
                 pass
-        S = max(lens, default=0)
         k = ops.dequantize_paged(pools[0], pools[1], pt, B, S, self.group_size, D, query_states.dtype)
         v = ops.dequantize_paged(pools[2], pools[3], pt, B, S, self.group_size, D, query_states.dtype)
-        uniform = all(n == S for n in lens)
         return ops.dense_attention(query_states, k, v, n_kv_heads=n_kv_heads, is_causal=is_causal,
                                    sm_scale=scale, seq_lens=None if uniform else seq_lens)
 

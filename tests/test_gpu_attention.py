@@ -146,6 +146,21 @@ def test_prefill_route_matches_oracle():
     assert np.abs(got - _as_written(q, kp, ks, vp, vs, 32, 2, causal=True)).max() <= 2e-2
 
 
+@pytest.mark.parametrize("Sq,causal", [(100, True), (100, False), (300, True), (300, False)])
+def test_query_blocks_on_both_routes(Sq, causal):
+    """Blocks of 400 query rows per KV head take the fused kernel (up to 1024
+    rows); 1200 rows take dequantize + flash SDPA, whose lower-right causal
+    variant aligns a block after cached tokens bottom-right (a prompt chunk or
+    a speculative block over a long cache)."""
+    Hq, Hkv, Sk = 8, 2, 700
+    assert (Hq // Hkv) * 100 <= ops.MAX_FUSED_ROWS < (Hq // Hkv) * 300
+    q, kp, ks, vp, vs = _inputs(1, Hq, Hkv, Sq, Sk, 128, "bf16", seed=Sq + causal)
+    out = attention_forward_quant_gqa(q.to(DEV), kp, ks, vp, vs, n_q_heads=Hq, n_kv_heads=Hkv, is_causal=causal)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - _oracle(q, kp, ks, vp, vs, 32, causal=causal)).max() <= 2e-2
+    assert np.abs(got - _as_written(q, kp, ks, vp, vs, 32, Hq // Hkv, causal=causal)).max() <= 2e-2
+
+
 def test_shape_outside_fused_kernel():
     q, kp, ks, vp, vs = _inputs(1, 4, 2, 1, 50, 96, "bf16", seed=3, G=16)
     out = attention_forward_quant_gqa(q.to(DEV), kp, ks, vp, vs, n_q_heads=4, n_kv_heads=2, group_size=16)
