@@ -196,6 +196,34 @@ int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
                     void* stream);
 
 /*
+ * kvq_prefill_attn — attention of a long query block (prompt prefill, or a
+ * prompt chunk after cached tokens) over an INT4 cache, on the matrix cores.
+ * Replaces the reference's fused GQA kernel at Sq > 1
+ * (kernels/llama3/attention_quant.py:159-286, launched by
+ * models/llama3/llama3_quant.py:74-88 for prompts) and, in this build, the
+ * dequantize + dense SDPA route for long blocks.
+ *
+ * Arguments and layouts as kvq_decode_attn, with one sequence length Sk for
+ * the whole batch (no seq_lens, no workspace). With is_causal, query row i may
+ * attend key j iff j <= Sk - Sq + i; a row with no admissible key yields
+ * zeros. K and V are dequantized to q's dtype ((n - 8) * scale, rounded to
+ * nearest even) and the products accumulate in fp32.
+ * Supported: bf16/fp16 q with bf16/fp16 scales, D in {64, 128}, group_size in
+ * {32, 64, 128} dividing D, Hq / Hkv dividing 64, q and out rows contiguous;
+ * KVQ_EUNSUP otherwise. B == 0 or Sq == 0 launches nothing.
+ */
+int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
+                     const void* k_packed, const int64_t* kp_strides,
+                     const void* k_scales, const int64_t* ks_strides,
+                     const void* v_packed, const int64_t* vp_strides,
+                     const void* v_scales, const int64_t* vs_strides,
+                     int scale_dtype,
+                     void* out, const int64_t* out_strides,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                     int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
+                     void* stream);
+
+/*
  * Paged caches.
  *
  * The reference keeps one contiguous tensor per layer and grows it with

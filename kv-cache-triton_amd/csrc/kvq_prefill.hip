@@ -1,0 +1,391 @@
+// Attention of long query blocks over the INT4 cache on the matrix cores
+// (gfx950): prompt prefill and prompt chunks after cached tokens.
+//
+// Reference: kernels/llama3/attention_quant.py:24-152 (_attention_fwd_quant_gqa_
+// _kernel) computes the same thing per (batch, query head, 16-query block):
+// dequantize 64-key tiles of K and V, scores q.k * d^-1/2, bottom-right causal
+// mask (:91-97, :123), online softmax, o += p.v. Here one workgroup takes 64
+// query rows of one KV head (GQA group x positions, so each K/V tile is read
+// once for the whole group), dequantizes each 64-key tile into LDS once for
+// its four waves, and runs both products on v_mfma_f32_16x16x32 bf16/f16.
+//
+// Layout of one wave's work (16 query rows, lane l: lq = l % 16, lg = l / 16;
+// MFMA 16x16x32: A[i][k] at lane (i, k / 8), register k % 8; B[k][n] at lane
+// (n, k / 8); C[i][n] at lane (n, i / 4), register i % 4):
+//   S^T = K Q^T   four 16-key blocks per 64-key tile, 32 dims per MFMA:
+//                 A = K rows from LDS, B = the wave's Q (registers, loaded
+//                 once). Block kb's row i is key 32 (kb / 2) + 8 (i / 4) +
+//                 4 (kb % 2) + i % 4, so lane (lq, lg) ends up holding the
+//                 scores of query row lq for keys 32 h + 8 lg .. + 7 in blocks
+//                 2 h and 2 h + 1;
+//   O^T += V^T P^T  A = V^T rows from LDS (V is stored transposed), B = P^T
+//                 over 32 keys, which is exactly what the lane holds, so the
+//                 softmax weights never leave the lane; lane (lq, lg)
+//                 accumulates dims 4 lg .. 4 lg + 3 of each 16-dim block of
+//                 query row lq.
+// Every per-row scalar (running max, sum, rescale) thus lives on the lanes of
+// that row: lq, lq + 16, lq + 32, lq + 48, combined with two xor shuffles.
+//
+// K and V are dequantized exactly as kvq_dequantize does ((n - 8) * scale in
+// fp32, rounded to the query dtype), i.e. the numerics of dequantize + SDPA.
+
+#include "kvq_common.h"
+
+namespace kvq {
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kRows = 64;    // query rows per workgroup (4 waves x 16)
+constexpr int kKeys = 64;    // keys per tile
+constexpr float kNegP = -1.0e30f;
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t qs_b, qs_h, qs_s;  // element strides (dims contiguous)
+  const uint8_t* kp;
+  int64_t kps_b, kps_h, kps_s;  // byte strides
+  const uint16_t* ks;
+  int64_t kss_b, kss_h, kss_s;  // element strides
+  const uint8_t* vp;
+  int64_t vps_b, vps_h, vps_s;
+  const uint16_t* vs;
+  int64_t vss_b, vss_h, vss_s;
+  uint16_t* out;
+  int64_t os_b, os_h, os_s;
+  int Hkv, ratio, Sq, Sk, G, row_blocks, causal;
+  float scale_log2;  // sm_scale * log2(e): scores in base 2
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t prefill_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma32(uint4 a, uint4 b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// two values rounded to the MFMA input type, packed low | high << 16
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (F16) {
+    const f16x2_t h = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+  } else {
+    const bf16x2_t h = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+
+template <bool S_F16>
+__device__ __forceinline__ float scale_f32(uint32_t bits) {
+  return S_F16 ? f16_bits_to_f32(bits & 0xffffu) : bf16_bits_to_f32(bits & 0xffffu);
+}
+
+template <int D, bool F16, bool S_F16>
+__global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) {
+  constexpr int KP = D + 8;      // K tile row pitch in LDS (elements)
+  constexpr int VP = kKeys + 8;  // V^T tile row pitch
+  constexpr int NK = D / 32;     // 32-dim steps of S^T
+  constexpr int NB = D / 16;     // 16-dim blocks of O^T
+  __shared__ __align__(16) uint16_t k_lds[kKeys * KP];
+  __shared__ __align__(16) uint16_t v_lds[D * VP];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lq = lane & 15, lg = lane >> 4;
+  // workgroup -> (KV head fastest, so that one head's row blocks share an
+  // XCD and its L2; row blocks with the most keys first; batch)
+  int wg = blockIdx.x;
+  const int kvh = wg % a.Hkv;
+  wg /= a.Hkv;
+  const int rb = a.row_blocks - 1 - wg % a.row_blocks;
+  const int b = wg / a.row_blocks;
+
+  // this lane's query row and the keys it may attend: [0, lim)
+  const int R = rb * kRows + wave * 16 + lq;
+  const int s = R / a.ratio;
+  const int head = kvh * a.ratio + R % a.ratio;
+  const bool row_ok = s < a.Sq;
+  int lim = row_ok ? (a.causal ? a.Sk - a.Sq + s + 1 : a.Sk) : 0;
+  lim = lim < 0 ? 0 : (lim > a.Sk ? a.Sk : lim);
+  // keys any row of the workgroup attends
+  const int r_last = min((rb + 1) * kRows, a.Sq * a.ratio) - 1;
+  int kend = a.causal ? a.Sk - a.Sq + r_last / a.ratio + 1 : a.Sk;
+  kend = kend < 0 ? 0 : (kend > a.Sk ? a.Sk : kend);
+  const int ntiles = (kend + kKeys - 1) / kKeys;
+
+  // the wave's queries as the B operand of S^T: lane (lq, lg) holds dims
+  // 32 kk + 8 lg .. + 7 of row lq (rows past Sq are zero)
+  uint4 qf[NK];
+  {
+    const uint16_t* qr = a.q + (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)(row_ok ? s : 0) * a.qs_s;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      const uint16_t* p = qr + 32 * kk + 8 * lg;
+      uint32_t x[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) x[w] = row_ok ? (uint32_t)p[2 * w] | ((uint32_t)p[2 * w + 1] << 16) : 0u;
+      qf[kk] = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+  }
+
+  // cache slices of this (batch, KV head) as bounds-checked buffers: rows at
+  // or past Sk read as zero
+  const uint32_t kps = (uint32_t)a.kps_s, vps = (uint32_t)a.vps_s;
+  const uint32_t kss2 = 2u * (uint32_t)a.kss_s, vss2 = 2u * (uint32_t)a.vss_s;
+  const uint32_t Sk = (uint32_t)a.Sk;
+  const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(a.kp + b * a.kps_b + kvh * a.kps_h, Sk * kps);
+  const __amdgpu_buffer_rsrc_t rks = prefill_rsrc(a.ks + b * a.kss_b + kvh * a.kss_h, Sk * kss2);
+  const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(a.vp + b * a.vps_b + kvh * a.vps_h, Sk * vps);
+  const __amdgpu_buffer_rsrc_t rvs = prefill_rsrc(a.vs + b * a.vss_b + kvh * a.vss_h, Sk * vss2);
+
+  // tile loaders. K: thread (key tid / 4, quarter tid % 4) takes D / 4 dims
+  // (D / 8 code bytes, one scale group). V: thread (keys 4 (tid % 16) .. + 3,
+  // dims (tid / 16) * D / 16 .. + D / 16) so that it writes V^T rows of four
+  // consecutive keys.
+  constexpr int KB = D / 8;    // K code bytes per thread
+  constexpr int VD = D / 16;   // V dims per thread
+  const int k_key = tid >> 2, k_q = tid & 3;
+  const int v_kq = tid & 15, v_dq = tid >> 4;
+  const uint32_t k_grp = (uint32_t)((k_q * (D / 4)) / a.G);
+  const uint32_t v_grp = (uint32_t)((v_dq * VD) / a.G);
+  uint32_t kraw[KB / 4];
+  uint32_t ksc;
+  uint32_t vraw[4];
+  uint32_t vsc[4];
+  auto load_tile = [&](uint32_t t0) {
+    const uint32_t kr = t0 + (uint32_t)k_key;
+    if constexpr (KB == 16) {
+      const u32x4_t w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, kr * kps + 16u * k_q, 0, 0));
+      kraw[0] = w.x; kraw[1] = w.y; kraw[2] = w.z; kraw[3] = w.w;
+    } else {
+      const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rk, kr * kps + 8u * k_q, 0, 0));
+      kraw[0] = w.x; kraw[1] = w.y;
+    }
+    ksc = __builtin_amdgcn_raw_buffer_load_b16(rks, kr * kss2 + 2u * k_grp, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t vr = t0 + 4u * (uint32_t)v_kq + (uint32_t)i;
+      if constexpr (VD == 8)
+        vraw[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, vr * vps + 4u * v_dq, 0, 0);
+      else
+        vraw[i] = __builtin_amdgcn_raw_buffer_load_b16(rv, vr * vps + 2u * v_dq, 0, 0);
+      vsc[i] = __builtin_amdgcn_raw_buffer_load_b16(rvs, vr * vss2 + 2u * v_grp, 0, 0);
+    }
+  };
+  auto store_tile = [&]() {
+    {  // K row k_key, dims k_q * D / 4 .. + D / 4 (element 2j of a byte's pair in the low nibble)
+      const float sc = scale_f32<S_F16>(ksc);
+      uint32_t pk[KB];
+#pragma unroll
+      for (int w = 0; w < KB / 4; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t byte = (kraw[w] >> (8 * j)) & 0xffu;
+          pk[4 * w + j] = pack2<F16>((float)((int)(byte & 15u) - 8) * sc, (float)((int)(byte >> 4) - 8) * sc);
+        }
+      uint16_t* dst = k_lds + k_key * KP + k_q * (D / 4);
+#pragma unroll
+      for (int w = 0; w < KB / 4; ++w)
+        *(uint4*)(dst + 8 * w) = make_uint4(pk[4 * w], pk[4 * w + 1], pk[4 * w + 2], pk[4 * w + 3]);
+    }
+    {  // V^T rows v_dq * VD + d, keys 4 v_kq .. + 3
+      float vf[4][VD];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sc = scale_f32<S_F16>(vsc[i]);
+#pragma unroll
+        for (int d = 0; d < VD; ++d) vf[i][d] = (float)((int)((vraw[i] >> (4 * d)) & 15u) - 8) * sc;
+      }
+#pragma unroll
+      for (int d = 0; d < VD; ++d)
+        *(uint2*)(v_lds + (v_dq * VD + d) * VP + 4 * v_kq) =
+            make_uint2(pack2<F16>(vf[0][d], vf[1][d]), pack2<F16>(vf[2][d], vf[3][d]));
+    }
+  };
+
+  f32x4_t o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kNegP, l_run = 0.0f;
+
+  if (ntiles > 0) load_tile(0u);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int t0 = tile * kKeys;
+    __syncthreads();  // every wave is done reading the previous tile
+    store_tile();
+    if (tile + 1 < ntiles) load_tile((uint32_t)(t0 + kKeys));
+    __syncthreads();
+
+    // ---- S^T = K Q^T, 4 blocks of 16 keys (block kb, row i: key
+    //      32 (kb / 2) + 8 (i / 4) + 4 (kb % 2) + i % 4) ----
+    f32x4_t st[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int krow = 32 * (kb >> 1) + 8 * (lq >> 2) + 4 * (kb & 1) + (lq & 3);
+      st[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        const uint4 ka = *(const uint4*)(k_lds + krow * KP + 32 * kk + 8 * lg);
+        st[kb] = mfma32<F16>(ka, qf[kk], st[kb]);
+      }
+    }
+    // ---- online softmax (base 2) for query row lq; register j of block kb
+    //      is key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j ----
+    const bool full = t0 + kKeys <= lim;  // no key of this tile is masked for this row
+    float mt = kNegP;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float x = st[kb][j] * a.scale_log2;
+        if (!full) x = t0 + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1) + j < lim ? x : kNegP;
+        st[kb][j] = x;
+        mt = fmaxf(mt, x);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
+    uint2 pf[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      float p[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(st[kb][j] - m_new);
+        if (!full) p[j] = st[kb][j] > kNegP ? p[j] : 0.0f;
+        l_run += p[j];
+      }
+      pf[kb] = make_uint2(pack2<F16>(p[0], p[1]), pack2<F16>(p[2], p[3]));
+    }
+    // ---- O^T += V^T P^T, 32 keys per MFMA: keys 32 h + 8 lg .. + 7 ----
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 va = *(const uint4*)(v_lds + (16 * nb + lq) * VP + 32 * h + 8 * lg);
+        const uint4 pb = make_uint4(pf[2 * h].x, pf[2 * h].y, pf[2 * h + 1].x, pf[2 * h + 1].y);
+        o[nb] = mfma32<F16>(va, pb, o[nb]);
+      }
+  }
+
+  // ---- normalise and store: lane (lq, lg) holds dims 16 nb + 4 lg .. + 3 ----
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (row_ok) {
+    uint16_t* orow = a.out + (int64_t)b * a.os_b + (int64_t)head * a.os_h + (int64_t)s * a.os_s;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint32_t w0 = pack2<F16>(o[nb][0] * inv, o[nb][1] * inv);
+      const uint32_t w1 = pack2<F16>(o[nb][2] * inv, o[nb][3] * inv);
+      uint16_t* p = orow + 16 * nb + 4 * lg;
+      p[0] = (uint16_t)w0; p[1] = (uint16_t)(w0 >> 16);
+      p[2] = (uint16_t)w1; p[3] = (uint16_t)(w1 >> 16);
+    }
+  }
+}
+
+template <int D, bool F16>
+void launch_prefill(const PrefillArgs& a, bool s_f16, dim3 grid, hipStream_t st) {
+  if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false>), grid, dim3(256), 0, st, a);
+}
+
+}  // namespace
+}  // namespace kvq
+
+using namespace kvq;
+
+extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
+                                const void* k_packed, const int64_t* kp_strides,
+                                const void* k_scales, const int64_t* ks_strides,
+                                const void* v_packed, const int64_t* vp_strides,
+                                const void* v_scales, const int64_t* vs_strides,
+                                int scale_dtype,
+                                void* out, const int64_t* out_strides,
+                                int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
+                                void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(q_strides && kp_strides && ks_strides && vp_strides && vs_strides && out_strides,
+                "kvq_prefill_attn: null stride array");
+  KVQ_CHECK_ARG(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && Hq % Hkv == 0,
+                "kvq_prefill_attn: bad shape (B=%lld Hq=%lld Hkv=%lld Sq=%lld Sk=%lld)", (long long)B,
+                (long long)Hq, (long long)Hkv, (long long)Sq, (long long)Sk);
+  if (!((q_dtype == KVQ_BF16 || q_dtype == KVQ_F16) && (scale_dtype == KVQ_BF16 || scale_dtype == KVQ_F16))) {
+    set_error("kvq_prefill_attn: bf16/fp16 queries and scales only");
+    return KVQ_EUNSUP;
+  }
+  const int64_t ratio = Hq / Hkv;
+  if (!(D == 64 || D == 128) || !(group_size == 32 || group_size == 64 || group_size == 128) ||
+      D % group_size != 0 || 64 % ratio != 0) {
+    set_error("kvq_prefill_attn: unsupported shape (D=%lld G=%lld Hq/Hkv=%lld)", (long long)D,
+              (long long)group_size, (long long)ratio);
+    return KVQ_EUNSUP;
+  }
+  if (q_strides[3] != 1 || out_strides[3] != 1) {
+    set_error("kvq_prefill_attn: q and out rows must be contiguous");
+    return KVQ_EUNSUP;
+  }
+  KVQ_CHECK_ARG(kp_strides[2] >= D / 2 && vp_strides[2] >= D / 2 && ks_strides[2] >= D / group_size &&
+                    vs_strides[2] >= D / group_size,
+                "kvq_prefill_attn: cache rows narrower than D / 2 code bytes or D / G scales");
+  if (Sk * kp_strides[2] >= (1ll << 31) || Sk * vp_strides[2] >= (1ll << 31) || Sk * ks_strides[2] * 2 >= (1ll << 31) ||
+      Sk * vs_strides[2] * 2 >= (1ll << 31)) {
+    set_error("kvq_prefill_attn: a (batch, head) slice of the cache exceeds 2 GiB");
+    return KVQ_EUNSUP;
+  }
+  if (B == 0 || Sq == 0) return KVQ_OK;
+  KVQ_CHECK_ARG(q && out && (Sk == 0 || (k_packed && k_scales && v_packed && v_scales)),
+                "kvq_prefill_attn: null data pointer");
+  const int64_t row_blocks = (Sq * ratio + kRows - 1) / kRows;
+  const int64_t n_wg = B * Hkv * row_blocks;
+  KVQ_CHECK_ARG(n_wg < (1ll << 31) && Sq < (1ll << 30) && Sk < (1ll << 30), "kvq_prefill_attn: too large");
+
+  PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.qs_b = q_strides[0]; a.qs_h = q_strides[1]; a.qs_s = q_strides[2];
+  a.kp = (const uint8_t*)k_packed;
+  a.kps_b = kp_strides[0]; a.kps_h = kp_strides[1]; a.kps_s = kp_strides[2];
+  a.ks = (const uint16_t*)k_scales;
+  a.kss_b = ks_strides[0]; a.kss_h = ks_strides[1]; a.kss_s = ks_strides[2];
+  a.vp = (const uint8_t*)v_packed;
+  a.vps_b = vp_strides[0]; a.vps_h = vp_strides[1]; a.vps_s = vp_strides[2];
+  a.vs = (const uint16_t*)v_scales;
+  a.vss_b = vs_strides[0]; a.vss_h = vs_strides[1]; a.vss_s = vs_strides[2];
+  a.out = (uint16_t*)out;
+  a.os_b = out_strides[0]; a.os_h = out_strides[1]; a.os_s = out_strides[2];
+  a.Hkv = (int)Hkv; a.ratio = (int)ratio; a.Sq = (int)Sq; a.Sk = (int)Sk; a.G = (int)group_size;
+  a.row_blocks = (int)row_blocks; a.causal = is_causal ? 1 : 0;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+
+  const dim3 grid((unsigned)n_wg);
+  hipStream_t st = (hipStream_t)stream;
+  const bool f16 = q_dtype == KVQ_F16, s_f16 = scale_dtype == KVQ_F16;
+  if (D == 128) {
+    if (f16) launch_prefill<128, true>(a, s_f16, grid, st);
+    else launch_prefill<128, false>(a, s_f16, grid, st);
+  } else {
+    if (f16) launch_prefill<64, true>(a, s_f16, grid, st);
+    else launch_prefill<64, false>(a, s_f16, grid, st);
+  }
+  KVQ_CHECK_LAUNCH("kvq_prefill_attn");
+  return KVQ_OK;
+}

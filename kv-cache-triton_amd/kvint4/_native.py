@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "kvq_dequantize_paged",
     "kvq_decode_attn_paged",
     "kvq_decode_step_paged",
+    "kvq_prefill_attn",
 )
 
 _lock = threading.Lock()
@@ -89,6 +90,15 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, ctypes.c_float,
         _i64, _vp, _i64, _vp,
+    ]
+    lib.kvq_prefill_attn.restype = _i32
+    lib.kvq_prefill_attn.argtypes = [
+        _vp, _i32, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _i32,
+        _vp, _i64p,
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        _i32, ctypes.c_float, _vp,
     ]
     # paged counterparts: (block_table, table_stride, table_cols, num_blocks,
     # page_size) after the cache arguments; pool strides are (head, row)

@@ -20,7 +20,7 @@ PKG_ROOT = os.path.dirname(_HERE)  # kv-cache-triton_amd/
 CSRC = os.path.join(PKG_ROOT, "csrc")
 OUT = os.path.join(_HERE, "libkvint4.so")
 
-SOURCES = ("kvq_capi.hip", "kvq_quant.hip", "kvq_attn.hip")
+SOURCES = ("kvq_capi.hip", "kvq_quant.hip", "kvq_attn.hip", "kvq_prefill.hip")
 ARCH = os.environ.get("KVQ_OFFLOAD_ARCH", "gfx950")
 
 # Packed-FP32 VALU forms are kept out of the generated code (the value path is

@@ -28,6 +28,14 @@ SUPPORTED_FLOATS = (torch.bfloat16, torch.float16, torch.float32)
 # faster route up to 1024 rows and flash SDPA beyond 2048, at 512 to 16K keys
 # (e.g. 16K keys, GQA 4: 256 queries 610 vs 652 us, 512 queries 1251 vs 654 us).
 MAX_FUSED_ROWS = 1024
+# Above this many rows per KV head, a block after cached tokens (Sq < Sk; a
+# prompt chunk) over a contiguous cache with one length for the batch goes to
+# the matrix-core prefill kernel instead (it dequantizes each 64-key tile into
+# LDS once for 64 rows): 16K keys, GQA 4, 256 queries 516 us vs 635 fused /
+# 668 dequantize + flash, 512 queries 538 vs 661 flash; 128 queries 513 vs
+# 325 fused. A whole prompt (Sq == Sk) stays on dequantize + flash SDPA,
+# 4.49 ms vs 4.65 ms at 16K.
+PREFILL_MIN_ROWS = 512
 
 
 def dense_fast_path(q: torch.Tensor, seq_lens: torch.Tensor | None) -> bool:
@@ -297,6 +305,54 @@ def fused_decode_attention(
     return out
 
 
+def prefill_attention(
+    q: torch.Tensor,
+    k_packed: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_packed: torch.Tensor,
+    v_scales: torch.Tensor,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    is_causal: bool,
+    sm_scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Long query blocks (prefill, prompt chunks) over the INT4 cache on the
+    matrix cores (kvq_prefill_attn); raises KVQUnsupported for shapes or
+    dtypes it does not handle. q [B, Hq, Sq, D]; K/V codes [B, Hkv, Sk, W],
+    one length Sk for the batch; causal masking aligned bottom-right."""
+    B, Hq, Sq, D = q.shape
+    Sk = k_packed.shape[2]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    if k_packed.stride(-1) != 1 or v_packed.stride(-1) != 1:
+        raise nat.KVQUnsupported("packed K/V last dim must be contiguous")
+    if k_scales.stride(-1) != 1:
+        k_scales = k_scales.contiguous()
+    if v_scales.stride(-1) != 1:
+        v_scales = v_scales.contiguous()
+    if v_scales.dtype != k_scales.dtype:
+        v_scales = v_scales.to(k_scales.dtype)
+    lib = nat.lib()
+    with nat.device_of(q):
+        rc = lib.kvq_prefill_attn(
+            q.data_ptr(), nat.DTYPE_CODE[q.dtype], nat.i64_array(q.stride()),
+            k_packed.data_ptr(), nat.i64_array(k_packed.stride()[:3]),
+            k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:3]),
+            v_packed.data_ptr(), nat.i64_array(v_packed.stride()[:3]),
+            v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:3]),
+            nat.DTYPE_CODE[k_scales.dtype],
+            out.data_ptr(), nat.i64_array(out.stride()),
+            B, Hq, n_kv_heads, Sq, D, group_size, Sk,
+            1 if is_causal else 0, float(sm_scale), nat.stream_handle(q.device),
+        )
+    nat.check(rc, "kvq_prefill_attn")
+    return out
+
+
 def decode_step(
     q: torch.Tensor,
     k_new: torch.Tensor,
@@ -498,12 +554,20 @@ def attention_over_quantized(
     sm_scale: float,
     seq_lens: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Route to the fused decode kernel when the query block is short (decode,
-    small speculative blocks) or when bottom-right causal masking is needed;
-    long blocks go to dequantize + dense SDPA."""
+    """Route by query rows per KV head: the fused decode kernel for short
+    blocks (decode, speculative blocks), the matrix-core prefill kernel for
+    long blocks after cached tokens (prompt chunks; one length for the
+    batch), and dequantize + dense SDPA for whole prompts and what neither
+    kernel takes."""
     B, Hq, Sq, D = q.shape
     Sk = k_packed.shape[2]
     rows = (Hq // n_kv_heads) * Sq
+    if rows > PREFILL_MIN_ROWS and seq_lens is None and Sq < Sk:
+        try:
+            return prefill_attention(q, k_packed, k_scales, v_packed, v_scales, n_kv_heads=n_kv_heads,
+                                     group_size=group_size, is_causal=is_causal, sm_scale=sm_scale)
+        except nat.KVQUnsupported:
+            pass
     use_fused = rows <= MAX_FUSED_ROWS or (is_causal and Sq != Sk and not dense_fast_path(q, seq_lens))
     if use_fused:
         try:

@@ -1,0 +1,87 @@
+"""GPU parity: the matrix-core prefill kernel (kvq_prefill_attn) vs the fp64
+oracle and vs the dequantize + dense SDPA route.
+
+Reference semantics (kernels/llama3/attention_quant.py:24-152, Sq > 1): GQA
+head map h // ratio, scores q.k * d^-1/2, causal mask aligned bottom-right
+(key j admissible for query i iff j <= Sk - Sq + i), online softmax over
+dequantized K/V. Bar: max-abs <= 2e-2 for bf16/fp16, as for the decode
+kernel (tests/llama3/test_attention_quant_gqa.py:58-91 uses 5e-2 for its
+prefill case). Cases: a prompt (Sq == Sk), prompt chunks after cached tokens,
+GQA ratios 1/4/8, head dims 64/128, group sizes 32/64/128, fp16, more queries
+than keys (rows with no admissible key are zero), an empty cache, and
+non-contiguous views of a larger cache.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from kvint4 import ops
+from oracle import kvq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TDT = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, G, seed, cap=None):
+    g = torch.Generator().manual_seed(seed)
+    t = TDT[dtype]
+    q = torch.randn(B, Hq, Sq, D, generator=g).to(t)
+    cap = cap or Sk
+    k = torch.randn(B, Hkv, cap, D, generator=g).to(t)
+    v = torch.randn(B, Hkv, cap, D, generator=g).to(t)
+    kp, ks = ops.quantize(k.to(DEV), G, t)
+    vp, vs = ops.quantize(v.to(DEV), G, t)
+    # views of the first Sk rows of a larger cache
+    return q, kp[:, :, :Sk], ks[:, :, :Sk], vp[:, :, :Sk], vs[:, :, :Sk]
+
+
+def _oracle(q, kp, ks, vp, vs, G, causal):
+    return O.attention_over_quantized(
+        q.float().numpy(), kp.cpu().numpy(), ks.float().cpu().numpy(), vp.cpu().numpy(),
+        vs.float().cpu().numpy(), group_size=G, is_causal=causal)
+
+
+CASES = [
+    # B, Hq, Hkv, Sq, Sk, D, G, dtype, causal
+    (2, 8, 2, 100, 100, 128, 32, "bf16", True),     # a prompt
+    (1, 32, 8, 300, 1000, 128, 32, "bf16", True),   # a chunk after 700 cached tokens
+    (1, 8, 8, 70, 200, 64, 64, "f16", False),       # MHA, D 64, G 64
+    (2, 16, 2, 33, 500, 128, 128, "bf16", True),    # GQA 8, G 128
+    (1, 4, 1, 129, 129, 64, 32, "f16", True),       # GQA 4, D 64, a row block cut short
+    (1, 8, 2, 200, 150, 128, 32, "bf16", True),     # more queries than keys
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,G,dtype,causal", CASES)
+def test_prefill_matches_oracle_and_dense_route(B, Hq, Hkv, Sq, Sk, D, G, dtype, causal):
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, G, seed=Sq * 7 + Sk, cap=Sk + 37)
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G,
+                                is_causal=causal, sm_scale=D ** -0.5)
+    got = out.float().cpu().numpy()
+    want = _oracle(q, kp, ks, vp, vs, G, causal)
+    err = np.abs(got - want).max()
+    print(f"prefill B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Sk={Sk} D={D} G={G} {dtype}: max-abs {err:.2e}")
+    assert err <= 2e-2, err
+    if causal and Sq > Sk:  # rows with no admissible key
+        assert np.all(got[:, :, : Sq - Sk] == 0)
+    dense = ops.dense_attention_over_quantized(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G,
+                                               is_causal=causal, sm_scale=D ** -0.5)
+    assert (out.float() - dense.float()).abs().max().item() <= 2e-2
+
+
+def test_prefill_empty_cache_and_unsupported():
+    q, kp, ks, vp, vs = _inputs(1, 8, 2, 16, 0, 128, "bf16", 32, seed=1, cap=8)
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=2, group_size=32, is_causal=False,
+                                sm_scale=0.1)
+    assert torch.all(out == 0)
+    from kvint4._native import KVQUnsupported
+
+    q32 = torch.randn(1, 8, 16, 128, device=DEV)
+    k = torch.randn(1, 2, 32, 128, device=DEV)
+    kp, ks = ops.quantize(k, 32, torch.float32)
+    with pytest.raises(KVQUnsupported):
+        ops.prefill_attention(q32, kp, ks, kp, ks, n_kv_heads=2, group_size=32, is_causal=True, sm_scale=0.1)
