@@ -93,8 +93,11 @@ __device__ __forceinline__ float scale_f32(uint32_t bits) {
   return S_F16 ? f16_bits_to_f32(bits & 0xffffu) : bf16_bits_to_f32(bits & 0xffffu);
 }
 
-template <int D, bool F16, bool S_F16>
+// RB = 16-row blocks per wave (1 or 2): with two, every K and V fragment read
+// from LDS feeds two MFMAs, halving LDS traffic and dequantize work per row.
+template <int D, bool F16, bool S_F16, int RB>
 __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) {
+  constexpr int ROWS = kRows * RB;  // query rows per workgroup
   constexpr int KP = D + 8;      // K tile row pitch in LDS (elements)
   constexpr int VP = kKeys + 8;  // V^T tile row pitch
   constexpr int NK = D / 32;     // 32-dim steps of S^T
@@ -109,34 +112,42 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
   int wg = blockIdx.x;
   const int kvh = wg % a.Hkv;
   wg /= a.Hkv;
-  const int rb = a.row_blocks - 1 - wg % a.row_blocks;
+  const int blk = a.row_blocks - 1 - wg % a.row_blocks;
   const int b = wg / a.row_blocks;
 
-  // this lane's query row and the keys it may attend: [0, lim)
-  const int R = rb * kRows + wave * 16 + lq;
-  const int s = R / a.ratio;
-  const int head = kvh * a.ratio + R % a.ratio;
-  const bool row_ok = s < a.Sq;
-  int lim = row_ok ? (a.causal ? a.Sk - a.Sq + s + 1 : a.Sk) : 0;
-  lim = lim < 0 ? 0 : (lim > a.Sk ? a.Sk : lim);
+  // this lane's query rows (one per row block) and the keys each may attend:
+  // [0, lim)
+  int s[RB], head[RB], lim[RB];
+  bool row_ok[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int R = blk * ROWS + wave * 16 * RB + 16 * r + lq;
+    s[r] = R / a.ratio;
+    head[r] = kvh * a.ratio + R % a.ratio;
+    row_ok[r] = s[r] < a.Sq;
+    int l = row_ok[r] ? (a.causal ? a.Sk - a.Sq + s[r] + 1 : a.Sk) : 0;
+    lim[r] = l < 0 ? 0 : (l > a.Sk ? a.Sk : l);
+  }
   // keys any row of the workgroup attends
-  const int r_last = min((rb + 1) * kRows, a.Sq * a.ratio) - 1;
+  const int r_last = min((blk + 1) * ROWS, a.Sq * a.ratio) - 1;
   int kend = a.causal ? a.Sk - a.Sq + r_last / a.ratio + 1 : a.Sk;
   kend = kend < 0 ? 0 : (kend > a.Sk ? a.Sk : kend);
   const int ntiles = (kend + kKeys - 1) / kKeys;
 
   // the wave's queries as the B operand of S^T: lane (lq, lg) holds dims
   // 32 kk + 8 lg .. + 7 of row lq (rows past Sq are zero)
-  uint4 qf[NK];
-  {
-    const uint16_t* qr = a.q + (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)(row_ok ? s : 0) * a.qs_s;
+  uint4 qf[RB][NK];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint16_t* qr =
+        a.q + (int64_t)b * a.qs_b + (int64_t)head[r] * a.qs_h + (int64_t)(row_ok[r] ? s[r] : 0) * a.qs_s;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       const uint16_t* p = qr + 32 * kk + 8 * lg;
       uint32_t x[4];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) x[w] = row_ok ? (uint32_t)p[2 * w] | ((uint32_t)p[2 * w + 1] << 16) : 0u;
-      qf[kk] = make_uint4(x[0], x[1], x[2], x[3]);
+      for (int w = 0; w < 4; ++w) x[w] = row_ok[r] ? (uint32_t)p[2 * w] | ((uint32_t)p[2 * w + 1] << 16) : 0u;
+      qf[r][kk] = make_uint4(x[0], x[1], x[2], x[3]);
     }
   }
 
@@ -215,10 +226,15 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
     }
   };
 
-  f32x4_t o[NB];
+  f32x4_t o[RB][NB];
+  float m_run[RB], l_run[RB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = kNegP, l_run = 0.0f;
+  for (int r = 0; r < RB; ++r) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o[r][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    m_run[r] = kNegP;
+    l_run[r] = 0.0f;
+  }
 
   if (ntiles > 0) load_tile(0u);
   for (int tile = 0; tile < ntiles; ++tile) {
@@ -230,49 +246,54 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
 
     // ---- S^T = K Q^T, 4 blocks of 16 keys (block kb, row i: key
     //      32 (kb / 2) + 8 (i / 4) + 4 (kb % 2) + i % 4) ----
-    f32x4_t st[4];
+    f32x4_t st[RB][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int krow = 32 * (kb >> 1) + 8 * (lq >> 2) + 4 * (kb & 1) + (lq & 3);
-      st[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int r = 0; r < RB; ++r) st[r][kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
         const uint4 ka = *(const uint4*)(k_lds + krow * KP + 32 * kk + 8 * lg);
-        st[kb] = mfma32<F16>(ka, qf[kk], st[kb]);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) st[r][kb] = mfma32<F16>(ka, qf[r][kk], st[r][kb]);
       }
     }
-    // ---- online softmax (base 2) for query row lq; register j of block kb
-    //      is key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j ----
-    const bool full = t0 + kKeys <= lim;  // no key of this tile is masked for this row
-    float mt = kNegP;
+    // ---- online softmax (base 2) per query row; register j of block kb is
+    //      key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j ----
+    uint2 pf[RB][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int r = 0; r < RB; ++r) {
+      const bool full = t0 + kKeys <= lim[r];  // no key of this tile is masked for this row
+      float mt = kNegP;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float x = st[kb][j] * a.scale_log2;
-        if (!full) x = t0 + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1) + j < lim ? x : kNegP;
-        st[kb][j] = x;
-        mt = fmaxf(mt, x);
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float x = st[r][kb][j] * a.scale_log2;
+          if (!full) x = t0 + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1) + j < lim[r] ? x : kNegP;
+          st[r][kb][j] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16));
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float m_new = fmaxf(m_run[r], mt);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[r] - m_new);
+      m_run[r] = m_new;
+      l_run[r] *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) o[r][nb] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        float p[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          p[j] = __builtin_amdgcn_exp2f(st[r][kb][j] - m_new);
+          if (!full) p[j] = st[r][kb][j] > kNegP ? p[j] : 0.0f;
+          l_run[r] += p[j];
+        }
+        pf[r][kb] = make_uint2(pack2<F16>(p[0], p[1]), pack2<F16>(p[2], p[3]));
       }
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
-    uint2 pf[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      float p[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(st[kb][j] - m_new);
-        if (!full) p[j] = st[kb][j] > kNegP ? p[j] : 0.0f;
-        l_run += p[j];
-      }
-      pf[kb] = make_uint2(pack2<F16>(p[0], p[1]), pack2<F16>(p[2], p[3]));
     }
     // ---- O^T += V^T P^T, 32 keys per MFMA: keys 32 h + 8 lg .. + 7 ----
 #pragma unroll
@@ -280,32 +301,44 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint4 va = *(const uint4*)(v_lds + (16 * nb + lq) * VP + 32 * h + 8 * lg);
-        const uint4 pb = make_uint4(pf[2 * h].x, pf[2 * h].y, pf[2 * h + 1].x, pf[2 * h + 1].y);
-        o[nb] = mfma32<F16>(va, pb, o[nb]);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          const uint4 pb = make_uint4(pf[r][2 * h].x, pf[r][2 * h].y, pf[r][2 * h + 1].x, pf[r][2 * h + 1].y);
+          o[r][nb] = mfma32<F16>(va, pb, o[r][nb]);
+        }
       }
   }
 
   // ---- normalise and store: lane (lq, lg) holds dims 16 nb + 4 lg .. + 3 ----
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (row_ok) {
-    uint16_t* orow = a.out + (int64_t)b * a.os_b + (int64_t)head * a.os_h + (int64_t)s * a.os_s;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const uint32_t w0 = pack2<F16>(o[nb][0] * inv, o[nb][1] * inv);
-      const uint32_t w1 = pack2<F16>(o[nb][2] * inv, o[nb][3] * inv);
-      uint16_t* p = orow + 16 * nb + 4 * lg;
-      p[0] = (uint16_t)w0; p[1] = (uint16_t)(w0 >> 16);
-      p[2] = (uint16_t)w1; p[3] = (uint16_t)(w1 >> 16);
+  for (int r = 0; r < RB; ++r) {
+    float l_tot = l_run[r] + __shfl_xor(l_run[r], 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (row_ok[r]) {
+      uint16_t* orow = a.out + (int64_t)b * a.os_b + (int64_t)head[r] * a.os_h + (int64_t)s[r] * a.os_s;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t w0 = pack2<F16>(o[r][nb][0] * inv, o[r][nb][1] * inv);
+        const uint32_t w1 = pack2<F16>(o[r][nb][2] * inv, o[r][nb][3] * inv);
+        uint16_t* p = orow + 16 * nb + 4 * lg;
+        p[0] = (uint16_t)w0; p[1] = (uint16_t)(w0 >> 16);
+        p[2] = (uint16_t)w1; p[3] = (uint16_t)(w1 >> 16);
+      }
     }
   }
 }
 
-template <int D, bool F16>
+template <int D, bool F16, int RB>
 void launch_prefill(const PrefillArgs& a, bool s_f16, dim3 grid, hipStream_t st) {
-  if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false>), grid, dim3(256), 0, st, a);
+  if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB>), grid, dim3(256), 0, st, a);
+}
+
+template <int D, bool F16>
+void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, dim3 grid, hipStream_t st) {
+  if (rb == 2) launch_prefill<D, F16, 2>(a, s_f16, grid, st);
+  else launch_prefill<D, F16, 1>(a, s_f16, grid, st);
 }
 
 }  // namespace
@@ -355,7 +388,10 @@ extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_str
   if (B == 0 || Sq == 0) return KVQ_OK;
   KVQ_CHECK_ARG(q && out && (Sk == 0 || (k_packed && k_scales && v_packed && v_scales)),
                 "kvq_prefill_attn: null data pointer");
-  const int64_t row_blocks = (Sq * ratio + kRows - 1) / kRows;
+  // two 16-row blocks per wave (128 rows per workgroup) once that still
+  // leaves two workgroups per CU of a 256-CU device; one otherwise
+  const int rb = B * Hkv * ((Sq * ratio + 2 * kRows - 1) / (2 * kRows)) >= 512 ? 2 : 1;
+  const int64_t row_blocks = (Sq * ratio + rb * kRows - 1) / (rb * kRows);
   const int64_t n_wg = B * Hkv * row_blocks;
   KVQ_CHECK_ARG(n_wg < (1ll << 31) && Sq < (1ll << 30) && Sk < (1ll << 30), "kvq_prefill_attn: too large");
 
@@ -380,11 +416,11 @@ extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_str
   hipStream_t st = (hipStream_t)stream;
   const bool f16 = q_dtype == KVQ_F16, s_f16 = scale_dtype == KVQ_F16;
   if (D == 128) {
-    if (f16) launch_prefill<128, true>(a, s_f16, grid, st);
-    else launch_prefill<128, false>(a, s_f16, grid, st);
+    if (f16) launch_prefill_rb<128, true>(a, s_f16, rb, grid, st);
+    else launch_prefill_rb<128, false>(a, s_f16, rb, grid, st);
   } else {
-    if (f16) launch_prefill<64, true>(a, s_f16, grid, st);
-    else launch_prefill<64, false>(a, s_f16, grid, st);
+    if (f16) launch_prefill_rb<64, true>(a, s_f16, rb, grid, st);
+    else launch_prefill_rb<64, false>(a, s_f16, rb, grid, st);
   }
   KVQ_CHECK_LAUNCH("kvq_prefill_attn");
   return KVQ_OK;

@@ -28,13 +28,12 @@ SUPPORTED_FLOATS = (torch.bfloat16, torch.float16, torch.float32)
 # faster route up to 1024 rows and flash SDPA beyond 2048, at 512 to 16K keys
 # (e.g. 16K keys, GQA 4: 256 queries 610 vs 652 us, 512 queries 1251 vs 654 us).
 MAX_FUSED_ROWS = 1024
-# Above this many rows per KV head, a block after cached tokens (Sq < Sk; a
-# prompt chunk) over a contiguous cache with one length for the batch goes to
-# the matrix-core prefill kernel instead (it dequantizes each 64-key tile into
-# LDS once for 64 rows): 16K keys, GQA 4, 256 queries 516 us vs 635 fused /
-# 668 dequantize + flash, 512 queries 538 vs 661 flash; 128 queries 513 vs
-# 325 fused. A whole prompt (Sq == Sk) stays on dequantize + flash SDPA,
-# 4.49 ms vs 4.65 ms at 16K.
+# Above this many rows per KV head, a block over a contiguous cache with one
+# length for the batch (a prompt, or a prompt chunk after cached tokens) goes
+# to the matrix-core prefill kernel instead (it dequantizes each 64-key tile
+# into LDS once for 64 or 128 rows): 16K keys, GQA 4, 256 queries 499 us vs
+# 614 fused / 664 dequantize + flash; a whole 16K prompt 4.06 ms vs 4.54 ms
+# flash; 128 queries 508 vs 323 fused.
 PREFILL_MIN_ROWS = 512
 
 
@@ -562,7 +561,7 @@ def attention_over_quantized(
     B, Hq, Sq, D = q.shape
     Sk = k_packed.shape[2]
     rows = (Hq // n_kv_heads) * Sq
-    if rows > PREFILL_MIN_ROWS and seq_lens is None and Sq < Sk:
+    if rows > PREFILL_MIN_ROWS and seq_lens is None:
         try:
             return prefill_attention(q, k_packed, k_scales, v_packed, v_scales, n_kv_heads=n_kv_heads,
                                      group_size=group_size, is_causal=is_causal, sm_scale=sm_scale)

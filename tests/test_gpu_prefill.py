@@ -85,3 +85,25 @@ def test_prefill_empty_cache_and_unsupported():
     kp, ks = ops.quantize(k, 32, torch.float32)
     with pytest.raises(KVQUnsupported):
         ops.prefill_attention(q32, kp, ks, kp, ks, n_kv_heads=2, group_size=32, is_causal=True, sm_scale=0.1)
+
+
+def test_prefill_two_row_blocks_per_wave():
+    """A launch of >= 512 workgroups takes two 16-row blocks per wave (128
+    rows per workgroup): the whole output against the dense route, and rows
+    across the block against the fp64 oracle (row i of a causal block after
+    cached tokens attends keys [0, Sk - Sq + i])."""
+    B, Hq, Hkv, Sq, Sk, D, G = 2, 32, 8, 1024, 3000, 128, 32
+    assert B * Hkv * (Sq * (Hq // Hkv) // 128) >= 512
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, "bf16", G, seed=11)
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=True,
+                                sm_scale=D ** -0.5)
+    dense = ops.dense_attention_over_quantized(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G,
+                                               is_causal=True, sm_scale=D ** -0.5)
+    assert (out.float() - dense.float()).abs().max().item() <= 2e-2
+    got = out.float().cpu().numpy()
+    for i in (0, 1, 37, 500, 1023):
+        n = Sk - Sq + i + 1
+        want = O.attention_over_quantized(
+            q[:, :, i:i + 1].float().numpy(), kp[:, :, :n].cpu().numpy(), ks[:, :, :n].float().cpu().numpy(),
+            vp[:, :, :n].cpu().numpy(), vs[:, :, :n].float().cpu().numpy(), group_size=G, is_causal=False)
+        assert np.abs(got[:, :, i:i + 1] - want).max() <= 2e-2, i
