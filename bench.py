@@ -84,6 +84,9 @@ def main() -> int:
     ap.add_argument("--paged", type=int, default=0, metavar="PAGE_SIZE",
                     help="keep each layer's cache in a block pool of PAGE_SIZE-row pages (>= 64, a power of "
                          "two) addressed through a block table, pages in a seeded random order; 0 = contiguous")
+    ap.add_argument("--prefill", type=int, default=0, metavar="SQ",
+                    help="time the matrix-core prefill kernel instead: a causal block of SQ query tokens "
+                         "over the workload's context (SQ == --ctx: a whole prompt), one JSON line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -122,6 +125,8 @@ def main() -> int:
         w["layers"] = args.layers
     if args.ctx:
         w["ctx"] = args.ctx
+    if args.prefill:
+        return prefill_bench(args, w)
     B, Hq, Hkv, D, G, ctx, L = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"], w["layers"]
     tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w["dtype"]]
     sdt = torch.float16 if w["dtype"] != "bf16" else torch.bfloat16  # GPT-2: fp16 scales
@@ -350,6 +355,77 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, layers, attended, seq_lens, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+    return 0
+
+
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 / fp16 matrix peak
+
+
+def prefill_bench(args, w: dict) -> int:
+    """Attention of a causal block of Sq query tokens over the workload's
+    context (Sk keys, the block's own tokens last) on kvq_prefill_attn, with
+    the dequantize + flash SDPA route timed beside it. Algorithmic work: QK
+    and PV over the admissible (bottom-right causal) key range, 4 * D flops
+    per (query head, query, key) pair. Four layers' caches are cycled."""
+    import torch
+
+    from kvint4 import ops
+
+    B, Hq, Hkv, D, G, Sk = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"]
+    Sq = min(args.prefill, Sk)
+    if w["dtype"] == "f32" or w["ragged"]:
+        print("bench.py: --prefill takes a 16-bit workload with one length for the batch", file=sys.stderr)
+        return 2
+    dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float16
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    layers = []
+    for _ in range(4):
+        kp, ks = ops.quantize(torch.randn(B, Hkv, Sk, D, device=dev, generator=gen).to(dt), G, dt)
+        vp, vs = ops.quantize(torch.randn(B, Hkv, Sk, D, device=dev, generator=gen).to(dt), G, dt)
+        q = torch.randn(B, Hq, Sq, D, device=dev, generator=gen).to(dt)
+        layers.append((q, kp, ks, vp, vs, torch.empty_like(q)))
+    kw = dict(n_kv_heads=Hkv, group_size=G, is_causal=True, sm_scale=D ** -0.5)
+
+    def step():
+        for q, kp, ks, vp, vs, o in layers:
+            ops.prefill_attention(q, kp, ks, vp, vs, out=o, **kw)
+
+    def dense_step():
+        for q, kp, ks, vp, vs, o in layers:
+            ops.dense_attention_over_quantized(q, kp, ks, vp, vs, **kw)
+
+    def timed(fn, n):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (n * len(layers))  # ms per layer
+
+    steps = max(1, min(args.steps, 20))
+    ms = timed(step, steps)
+    ms_dense = timed(dense_step, max(1, steps // 2))
+    err = (layers[0][5].float() - ops.dense_attention_over_quantized(*layers[0][:5], **kw).float()).abs().max().item()
+    pairs = sum(min(Sk, Sk - Sq + i + 1) for i in range(Sq))  # admissible (query, key) pairs per head
+    flops = 4.0 * B * Hq * D * pairs
+    tfs = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "INT4-KV prefill attention TFLOP/s (matrix cores)", "value": round(tfs, 1), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
+        "data": "synthetic (seeded torch.randn K/V/q, quantized by the HIP kernel)",
+        "config": {"workload": f"{w['desc'].replace('decode', 'prefill')}", "batch": B, "q_heads": Hq,
+                   "kv_heads": Hkv, "head_dim": D, "group_size": G, "context": Sk, "query_tokens": Sq,
+                   "causal": True},
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4), "traffic": None, "kernel": "prefill_attn_kernel"},
+        "dequant_flash_ms_per_layer": round(ms_dense, 4), "max_abs_vs_dequant_flash": err,
+    }), flush=True)
     return 0
 
 
