@@ -300,6 +300,22 @@ int kvq_decode_step_paged(const void* q, int q_dtype, const int64_t* q_strides,
                           int64_t n_split, void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* kvq_prefill_attn over a paged cache: every sequence attends its first Sk
+ * tokens (Sk <= table_cols * page_size); page_size >= 64. A key whose page has
+ * no block reads as zero codes and scales (score 0, value 0). */
+int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,
+                           const void* k_pool, const int64_t* kp_strides,
+                           const void* k_scale_pool, const int64_t* ks_strides,
+                           const void* v_pool, const int64_t* vp_strides,
+                           const void* v_scale_pool, const int64_t* vs_strides,
+                           int scale_dtype,
+                           const int32_t* block_table, int64_t table_stride, int64_t table_cols,
+                           int64_t num_blocks, int64_t page_size,
+                           void* out, const int64_t* out_strides,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                           int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,14 @@ struct PrefillArgs {
   int64_t os_b, os_h, os_s;
   int Hkv, ratio, Sq, Sk, G, row_blocks, causal;
   float scale_log2;  // sm_scale * log2(e): scores in base 2
+  // paged cache: K/V are pools [Hkv, n_blocks << page_shift, .] (batch
+  // strides 0); sequence b's token t is pool row bt[b * bt_stride +
+  // (t >> page_shift)] << page_shift | (t & (page size - 1)); entries outside
+  // [0, n_blocks), or pages >= bt_cols, have no rows. Pages hold a multiple of
+  // 64 rows, so a 64-key tile lies in one page.
+  const int32_t* bt;
+  int64_t bt_stride;
+  int bt_cols, n_blocks, page_shift;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t prefill_rsrc(const void* p, uint32_t bytes) {
@@ -95,7 +103,7 @@ __device__ __forceinline__ float scale_f32(uint32_t bits) {
 
 // RB = 16-row blocks per wave (1 or 2): with two, every K and V fragment read
 // from LDS feeds two MFMAs, halving LDS traffic and dequantize work per row.
-template <int D, bool F16, bool S_F16, int RB>
+template <int D, bool F16, bool S_F16, int RB, bool PAGED>
 __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int ROWS = kRows * RB;  // query rows per workgroup
   constexpr int KP = D + 8;      // K tile row pitch in LDS (elements)
@@ -156,10 +164,15 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
   const uint32_t kps = (uint32_t)a.kps_s, vps = (uint32_t)a.vps_s;
   const uint32_t kss2 = 2u * (uint32_t)a.kss_s, vss2 = 2u * (uint32_t)a.vss_s;
   const uint32_t Sk = (uint32_t)a.Sk;
-  const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(a.kp + b * a.kps_b + kvh * a.kps_h, Sk * kps);
-  const __amdgpu_buffer_rsrc_t rks = prefill_rsrc(a.ks + b * a.kss_b + kvh * a.kss_h, Sk * kss2);
-  const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(a.vp + b * a.vps_b + kvh * a.vps_h, Sk * vps);
-  const __amdgpu_buffer_rsrc_t rvs = prefill_rsrc(a.vs + b * a.vss_b + kvh * a.vss_h, Sk * vss2);
+  const uint8_t* kp_bh = a.kp + b * a.kps_b + kvh * a.kps_h;
+  const uint8_t* ks_bh = (const uint8_t*)(a.ks + b * a.kss_b + kvh * a.kss_h);
+  const uint8_t* vp_bh = a.vp + b * a.vps_b + kvh * a.vps_h;
+  const uint8_t* vs_bh = (const uint8_t*)(a.vs + b * a.vss_b + kvh * a.vss_h);
+  const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(kp_bh, Sk * kps);
+  const __amdgpu_buffer_rsrc_t rks = prefill_rsrc(ks_bh, Sk * kss2);
+  const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vp_bh, Sk * vps);
+  const __amdgpu_buffer_rsrc_t rvs = prefill_rsrc(vs_bh, Sk * vss2);
+  const int32_t* bt_b = PAGED ? a.bt + (int64_t)b * a.bt_stride : nullptr;
 
   // tile loaders. K: thread (key tid / 4, quarter tid % 4) takes D / 4 dims
   // (D / 8 code bytes, one scale group). V: thread (keys 4 (tid % 16) .. + 3,
@@ -176,23 +189,41 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
   uint32_t vraw[4];
   uint32_t vsc[4];
   auto load_tile = [&](uint32_t t0) {
-    const uint32_t kr = t0 + (uint32_t)k_key;
+    // contiguous: the slice's buffers at row t0. Paged: buffers over the
+    // tile's own rows (its page's pool rows from the first one), holding the
+    // keys before Sk, or none if no block holds the page.
+    __amdgpu_buffer_rsrc_t tk = rk, tks = rks, tv = rv, tvs = rvs;
+    uint32_t r0 = t0;
+    if constexpr (PAGED) {
+      const uint32_t pg = t0 >> a.page_shift;
+      const int32_t blk = __builtin_amdgcn_readfirstlane(pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1);
+      const bool ok = blk >= 0 && blk < a.n_blocks && t0 < Sk;
+      const uint32_t rb = __builtin_amdgcn_readfirstlane(
+          ok ? ((uint32_t)blk << a.page_shift) | (t0 & ((1u << a.page_shift) - 1u)) : 0u);
+      const uint32_t lim = __builtin_amdgcn_readfirstlane(ok ? min((uint32_t)kKeys, Sk - t0) : 0u);
+      tk = prefill_rsrc(kp_bh + (size_t)rb * kps, lim * kps);
+      tks = prefill_rsrc(ks_bh + (size_t)rb * kss2, lim * kss2);
+      tv = prefill_rsrc(vp_bh + (size_t)rb * vps, lim * vps);
+      tvs = prefill_rsrc(vs_bh + (size_t)rb * vss2, lim * vss2);
+      r0 = 0;
+    }
+    const uint32_t kr = r0 + (uint32_t)k_key;
     if constexpr (KB == 16) {
-      const u32x4_t w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, kr * kps + 16u * k_q, 0, 0));
+      const u32x4_t w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(tk, kr * kps + 16u * k_q, 0, 0));
       kraw[0] = w.x; kraw[1] = w.y; kraw[2] = w.z; kraw[3] = w.w;
     } else {
-      const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rk, kr * kps + 8u * k_q, 0, 0));
+      const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(tk, kr * kps + 8u * k_q, 0, 0));
       kraw[0] = w.x; kraw[1] = w.y;
     }
-    ksc = __builtin_amdgcn_raw_buffer_load_b16(rks, kr * kss2 + 2u * k_grp, 0, 0);
+    ksc = __builtin_amdgcn_raw_buffer_load_b16(tks, kr * kss2 + 2u * k_grp, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t vr = t0 + 4u * (uint32_t)v_kq + (uint32_t)i;
+      const uint32_t vr = r0 + 4u * (uint32_t)v_kq + (uint32_t)i;
       if constexpr (VD == 8)
-        vraw[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, vr * vps + 4u * v_dq, 0, 0);
+        vraw[i] = __builtin_amdgcn_raw_buffer_load_b32(tv, vr * vps + 4u * v_dq, 0, 0);
       else
-        vraw[i] = __builtin_amdgcn_raw_buffer_load_b16(rv, vr * vps + 2u * v_dq, 0, 0);
-      vsc[i] = __builtin_amdgcn_raw_buffer_load_b16(rvs, vr * vss2 + 2u * v_grp, 0, 0);
+        vraw[i] = __builtin_amdgcn_raw_buffer_load_b16(tv, vr * vps + 2u * v_dq, 0, 0);
+      vsc[i] = __builtin_amdgcn_raw_buffer_load_b16(tvs, vr * vss2 + 2u * v_grp, 0, 0);
     }
   };
   auto store_tile = [&]() {
@@ -331,8 +362,13 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
 
 template <int D, bool F16, int RB>
 void launch_prefill(const PrefillArgs& a, bool s_f16, dim3 grid, hipStream_t st) {
-  if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB>), grid, dim3(256), 0, st, a);
+  if (a.bt) {
+    if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB, false>), grid, dim3(256), 0, st, a);
+  }
 }
 
 template <int D, bool F16>
@@ -346,19 +382,22 @@ void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, dim3 grid, hipS
 
 using namespace kvq;
 
-extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
-                                const void* k_packed, const int64_t* kp_strides,
-                                const void* k_scales, const int64_t* ks_strides,
-                                const void* v_packed, const int64_t* vp_strides,
-                                const void* v_scales, const int64_t* vs_strides,
-                                int scale_dtype,
-                                void* out, const int64_t* out_strides,
-                                int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
-                                int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
-                                void* stream) {
-  clear_error();
-  KVQ_CHECK_ARG(q_strides && kp_strides && ks_strides && vp_strides && vs_strides && out_strides,
-                "kvq_prefill_attn: null stride array");
+namespace {
+
+struct PrefillPaged {
+  const int32_t* bt;
+  int64_t bt_stride, bt_cols, n_blocks, page_size;
+};
+
+// Shared by the contiguous and paged entry points. Strides are [3] (batch,
+// head, row); the paged entry point passes batch strides of 0.
+int prefill_impl(const void* q, int q_dtype, const int64_t* q_strides, const void* k_packed,
+                 const int64_t* kp_strides, const void* k_scales, const int64_t* ks_strides,
+                 const void* v_packed, const int64_t* vp_strides, const void* v_scales,
+                 const int64_t* vs_strides, int scale_dtype, void* out, const int64_t* out_strides, int64_t B,
+                 int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, int64_t group_size, int64_t Sk,
+                 int is_causal, float sm_scale, void* stream, const PrefillPaged* pg) {
+  KVQ_CHECK_ARG(q_strides && out_strides, "kvq_prefill_attn: null stride array");
   KVQ_CHECK_ARG(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && Hq % Hkv == 0,
                 "kvq_prefill_attn: bad shape (B=%lld Hq=%lld Hkv=%lld Sq=%lld Sk=%lld)", (long long)B,
                 (long long)Hq, (long long)Hkv, (long long)Sq, (long long)Sk);
@@ -380,10 +419,23 @@ extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_str
   KVQ_CHECK_ARG(kp_strides[2] >= D / 2 && vp_strides[2] >= D / 2 && ks_strides[2] >= D / group_size &&
                     vs_strides[2] >= D / group_size,
                 "kvq_prefill_attn: cache rows narrower than D / 2 code bytes or D / G scales");
-  if (Sk * kp_strides[2] >= (1ll << 31) || Sk * vp_strides[2] >= (1ll << 31) || Sk * ks_strides[2] * 2 >= (1ll << 31) ||
-      Sk * vs_strides[2] * 2 >= (1ll << 31)) {
-    set_error("kvq_prefill_attn: a (batch, head) slice of the cache exceeds 2 GiB");
+  // rows addressed through one buffer: a (batch, head) slice, or a head's pool
+  const int64_t rows_addr = pg ? pg->n_blocks * pg->page_size : Sk;
+  if (rows_addr * kp_strides[2] >= (1ll << 31) || rows_addr * vp_strides[2] >= (1ll << 31) ||
+      rows_addr * ks_strides[2] * 2 >= (1ll << 31) || rows_addr * vs_strides[2] * 2 >= (1ll << 31)) {
+    set_error("kvq_prefill_attn: a (batch, head) slice of the cache (or a head's pool) exceeds 2 GiB");
     return KVQ_EUNSUP;
+  }
+  int page_shift = 0;
+  if (pg) {
+    KVQ_CHECK_ARG(pg->page_size >= 64 && (pg->page_size & (pg->page_size - 1)) == 0 && pg->page_size <= (1 << 20),
+                  "kvq_prefill_attn_paged: page_size must be a power of two >= 64 (got %lld)",
+                  (long long)pg->page_size);
+    KVQ_CHECK_ARG(pg->n_blocks >= 0 && pg->n_blocks < (1ll << 31) && pg->bt_cols >= 0 && pg->bt_cols < (1ll << 31) &&
+                      pg->bt_stride >= pg->bt_cols && Sk <= pg->bt_cols * pg->page_size,
+                  "kvq_prefill_attn_paged: bad block table geometry or Sk past the table");
+    KVQ_CHECK_ARG(pg->bt != nullptr || pg->bt_cols == 0 || B == 0, "kvq_prefill_attn_paged: null block table");
+    while ((int64_t(1) << page_shift) < pg->page_size) ++page_shift;
   }
   if (B == 0 || Sq == 0) return KVQ_OK;
   KVQ_CHECK_ARG(q && out && (Sk == 0 || (k_packed && k_scales && v_packed && v_scales)),
@@ -411,6 +463,13 @@ extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_str
   a.Hkv = (int)Hkv; a.ratio = (int)ratio; a.Sq = (int)Sq; a.Sk = (int)Sk; a.G = (int)group_size;
   a.row_blocks = (int)row_blocks; a.causal = is_causal ? 1 : 0;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  // a paged call with no table columns maps no key: it runs as an empty cache
+  a.bt = (pg && pg->bt_cols > 0) ? pg->bt : nullptr;
+  a.bt_stride = pg ? pg->bt_stride : 0;
+  a.bt_cols = pg ? (int)pg->bt_cols : 0;
+  a.n_blocks = pg ? (int)pg->n_blocks : 0;
+  a.page_shift = page_shift;
+  if (pg && pg->bt_cols == 0) a.Sk = 0;
 
   const dim3 grid((unsigned)n_wg);
   hipStream_t st = (hipStream_t)stream;
@@ -424,4 +483,45 @@ extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_str
   }
   KVQ_CHECK_LAUNCH("kvq_prefill_attn");
   return KVQ_OK;
+}
+
+}  // namespace
+
+extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
+                                const void* k_packed, const int64_t* kp_strides,
+                                const void* k_scales, const int64_t* ks_strides,
+                                const void* v_packed, const int64_t* vp_strides,
+                                const void* v_scales, const int64_t* vs_strides,
+                                int scale_dtype,
+                                void* out, const int64_t* out_strides,
+                                int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
+                                void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(kp_strides && ks_strides && vp_strides && vs_strides, "kvq_prefill_attn: null stride array");
+  return prefill_impl(q, q_dtype, q_strides, k_packed, kp_strides, k_scales, ks_strides, v_packed, vp_strides,
+                      v_scales, vs_strides, scale_dtype, out, out_strides, B, Hq, Hkv, Sq, D, group_size, Sk,
+                      is_causal, sm_scale, stream, nullptr);
+}
+
+extern "C" int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,
+                                      const void* k_pool, const int64_t* kp_strides,
+                                      const void* k_scale_pool, const int64_t* ks_strides,
+                                      const void* v_pool, const int64_t* vp_strides,
+                                      const void* v_scale_pool, const int64_t* vs_strides,
+                                      int scale_dtype,
+                                      const int32_t* block_table, int64_t table_stride,
+                                      int64_t table_cols, int64_t num_blocks, int64_t page_size,
+                                      void* out, const int64_t* out_strides,
+                                      int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                      int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
+                                      void* stream) {
+  clear_error();
+  KVQ_CHECK_ARG(kp_strides && ks_strides && vp_strides && vs_strides, "kvq_prefill_attn_paged: null stride array");
+  const int64_t kp3[3] = {0, kp_strides[0], kp_strides[1]}, ks3[3] = {0, ks_strides[0], ks_strides[1]};
+  const int64_t vp3[3] = {0, vp_strides[0], vp_strides[1]}, vs3[3] = {0, vs_strides[0], vs_strides[1]};
+  const PrefillPaged pg{block_table, table_stride, table_cols, num_blocks, page_size};
+  return prefill_impl(q, q_dtype, q_strides, k_pool, kp3, k_scale_pool, ks3, v_pool, vp3, v_scale_pool, vs3,
+                      scale_dtype, out, out_strides, B, Hq, Hkv, Sq, D, group_size, Sk, is_causal, sm_scale,
+                      stream, &pg);
 }

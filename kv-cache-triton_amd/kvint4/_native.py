@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_attn_paged",
     "kvq_decode_step_paged",
     "kvq_prefill_attn",
+    "kvq_prefill_attn_paged",
 )
 
 _lock = threading.Lock()
@@ -103,6 +104,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     # paged counterparts: (block_table, table_stride, table_cols, num_blocks,
     # page_size) after the cache arguments; pool strides are (head, row)
     pg = [_vp, _i64, _i64, _i64, _i64]
+    lib.kvq_prefill_attn_paged.restype = _i32
+    lib.kvq_prefill_attn_paged.argtypes = [
+        _vp, _i32, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _i32, *pg,
+        _vp, _i64p,
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        _i32, ctypes.c_float, _vp,
+    ]
     lib.kvq_quantize_paged.restype = _i32
     lib.kvq_quantize_paged.argtypes = [
         _vp, _i32, _i64p, _i64, _i64, _i64, _i64, _i64,

@@ -779,6 +779,55 @@ def fused_decode_attention_paged(
     return out
 
 
+def prefill_attention_paged(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_pool: torch.Tensor,
+    v_scales: torch.Tensor,
+    pt: PageTable,
+    seq_len: int,
+    *,
+    n_kv_heads: int,
+    group_size: int,
+    is_causal: bool,
+    sm_scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """prefill_attention over a paged cache: every sequence attends its first
+    seq_len tokens through the block table (pages of >= 64 rows); raises
+    KVQUnsupported for shapes or dtypes the kernel does not handle."""
+    _check_cuda(q, k_pool, v_pool, pt.table, what="prefill_attention_paged")
+    B, Hq, Sq, D = q.shape
+    if pt.table.shape[0] < B:
+        raise ValueError("block table has fewer rows than the batch")
+    _check_pool(k_pool, k_scales, pt, n_kv_heads, D, group_size)
+    _check_pool(v_pool, v_scales, pt, n_kv_heads, D, group_size)
+    if not 0 <= seq_len <= pt.capacity:
+        raise ValueError(f"seq_len {seq_len} outside [0, {pt.capacity}]")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    if v_scales.dtype != k_scales.dtype:
+        raise nat.KVQUnsupported("K and V scales must share a dtype")
+    lib = nat.lib()
+    with nat.device_of(q):
+        rc = lib.kvq_prefill_attn_paged(
+            q.data_ptr(), nat.DTYPE_CODE[q.dtype], nat.i64_array(q.stride()),
+            k_pool.data_ptr(), nat.i64_array(k_pool.stride()[:2]),
+            k_scales.data_ptr(), nat.i64_array(k_scales.stride()[:2]),
+            v_pool.data_ptr(), nat.i64_array(v_pool.stride()[:2]),
+            v_scales.data_ptr(), nat.i64_array(v_scales.stride()[:2]),
+            nat.DTYPE_CODE[k_scales.dtype], *pt.args(),
+            out.data_ptr(), nat.i64_array(out.stride()),
+            B, Hq, n_kv_heads, Sq, D, group_size, seq_len,
+            1 if is_causal else 0, float(sm_scale), nat.stream_handle(q.device),
+        )
+    nat.check(rc, "kvq_prefill_attn_paged")
+    return out
+
+
 def decode_step_paged(
     q: torch.Tensor,
     k_new: torch.Tensor,

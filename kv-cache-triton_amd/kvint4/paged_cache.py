@@ -297,8 +297,9 @@ class PagedQuantizedKVCache:
                is_causal: bool) -> torch.Tensor:
         """Attention of query_states [B, H_q, S_q, d] over each sequence's
         cached tokens (causal: bottom-right aligned to each length). Short
-        query blocks run the paged fused kernel; long ones, or dtypes it does
-        not take, dequantize the pages and run dense SDPA."""
+        query blocks run the paged fused decode kernel; long ones with one
+        length for the batch the paged prefill kernel; what neither takes
+        dequantizes the pages and runs dense SDPA."""
         pools = self._pools[layer_idx]
         pt = self._page_table()
         seq_lens = self._seq_lens[layer_idx]
@@ -308,6 +309,13 @@ class PagedQuantizedKVCache:
         S = max(lens, default=0)
         uniform = all(n == S for n in lens)
         dense_fast = ops.dense_fast_path(query_states, None if uniform else seq_lens)
+        if self.page_size >= 64 and uniform and rows > ops.PREFILL_MIN_ROWS:
+            try:
+                return ops.prefill_attention_paged(
+                    query_states, *pools, pt, S, n_kv_heads=n_kv_heads, group_size=self.group_size,
+                    is_causal=is_causal, sm_scale=scale)
+            except _native.KVQUnsupported:
+                pass
         if self.page_size >= 64 and (rows <= ops.MAX_FUSED_ROWS or not dense_fast):
             try:
                 return ops.fused_decode_attention_paged(
