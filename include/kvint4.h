@@ -204,14 +204,21 @@ int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
  * dequantize + dense SDPA route for long blocks.
  *
  * Arguments and layouts as kvq_decode_attn, with one sequence length Sk for
- * the whole batch (no seq_lens, no workspace). With is_causal, query row i may
+ * the whole batch (no seq_lens). With is_causal, query row i may
  * attend key j iff j <= Sk - Sq + i; a row with no admissible key yields
  * zeros. K and V are dequantized to q's dtype ((n - 8) * scale, rounded to
  * nearest even) and the products accumulate in fp32.
  * Supported: bf16/fp16 q with bf16/fp16 scales, D in {64, 128}, group_size in
  * {32, 64, 128} dividing D, Hq / Hkv dividing 64, q and out rows contiguous;
  * KVQ_EUNSUP otherwise. B == 0 or Sq == 0 launches nothing.
+ * workspace: device scratch of kvq_prefill_attn_workspace_bytes(...) bytes
+ * (no initialisation needed). When the launch would be too small to fill
+ * the device, the key range is split and the splits' partials are merged in
+ * a second launch through it; NULL (or too small) runs unsplit. Calls that
+ * overlap in time must not share a workspace.
  */
+int64_t kvq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                         int64_t Sk);
 int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
                      const void* k_packed, const int64_t* kp_strides,
                      const void* k_scales, const int64_t* ks_strides,
@@ -221,7 +228,7 @@ int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
                      void* out, const int64_t* out_strides,
                      int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
                      int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
-                     void* stream);
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Paged caches.
@@ -314,7 +321,7 @@ int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,
                            void* out, const int64_t* out_strides,
                            int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
                            int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
-                           void* stream);
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,8 @@
 // K and V are dequantized exactly as kvq_dequantize does ((n - 8) * scale in
 // fp32, rounded to the query dtype), i.e. the numerics of dequantize + SDPA.
 
+#include <algorithm>
+
 #include "kvq_common.h"
 
 namespace kvq {
@@ -68,6 +70,12 @@ struct PrefillArgs {
   const int32_t* bt;
   int64_t bt_stride;
   int bt_cols, n_blocks, page_shift;
+  // split over keys (n_split > 1): workgroup split sp of a row block takes an
+  // equal share of its 64-key tiles and writes fp32 partials — unnormalised
+  // O rows [D] and (running max, sum) — for prefill_merge_kernel
+  int n_split;
+  float* ws_o;   // [unit][split][rows][D]
+  float* ws_ml;  // [unit][split][rows][2]
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t prefill_rsrc(const void* p, uint32_t bytes) {
@@ -103,8 +111,11 @@ __device__ __forceinline__ float scale_f32(uint32_t bits) {
 
 // RB = 16-row blocks per wave (1 or 2): with two, every K and V fragment read
 // from LDS feeds two MFMAs, halving LDS traffic and dequantize work per row.
+// Two row blocks per wave must stay within 256 registers (two waves per
+// SIMD, two workgroups per CU): one more register halves the occupancy.
 template <int D, bool F16, bool S_F16, int RB, bool PAGED>
-__global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RB == 2 ? 2 : 1)))
+void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int ROWS = kRows * RB;  // query rows per workgroup
   constexpr int KP = D + 8;      // K tile row pitch in LDS (elements)
   constexpr int VP = kKeys + 8;  // V^T tile row pitch
@@ -120,6 +131,8 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
   int wg = blockIdx.x;
   const int kvh = wg % a.Hkv;
   wg /= a.Hkv;
+  const int sp = wg % a.n_split;
+  wg /= a.n_split;
   const int blk = a.row_blocks - 1 - wg % a.row_blocks;
   const int b = wg / a.row_blocks;
 
@@ -140,7 +153,11 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
   const int r_last = min((blk + 1) * ROWS, a.Sq * a.ratio) - 1;
   int kend = a.causal ? a.Sk - a.Sq + r_last / a.ratio + 1 : a.Sk;
   kend = kend < 0 ? 0 : (kend > a.Sk ? a.Sk : kend);
-  const int ntiles = (kend + kKeys - 1) / kKeys;
+  // this split's tiles of the row block's key range
+  const int tiles_all = (kend + kKeys - 1) / kKeys;
+  const int tps = (tiles_all + a.n_split - 1) / a.n_split;
+  const int tile_lo = sp * tps;
+  const int tile_hi = min(tiles_all, tile_lo + tps);
 
   // the wave's queries as the B operand of S^T: lane (lq, lg) holds dims
   // 32 kk + 8 lg .. + 7 of row lq (rows past Sq are zero)
@@ -267,12 +284,12 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
     l_run[r] = 0.0f;
   }
 
-  if (ntiles > 0) load_tile(0u);
-  for (int tile = 0; tile < ntiles; ++tile) {
+  if (tile_lo < tile_hi) load_tile((uint32_t)(tile_lo * kKeys));
+  for (int tile = tile_lo; tile < tile_hi; ++tile) {
     const int t0 = tile * kKeys;
     __syncthreads();  // every wave is done reading the previous tile
     store_tile();
-    if (tile + 1 < ntiles) load_tile((uint32_t)(t0 + kKeys));
+    if (tile + 1 < tile_hi) load_tile((uint32_t)(t0 + kKeys));
     __syncthreads();
 
     // ---- S^T = K Q^T, 4 blocks of 16 keys (block kb, row i: key
@@ -345,6 +362,16 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
   for (int r = 0; r < RB; ++r) {
     float l_tot = l_run[r] + __shfl_xor(l_run[r], 16);
     l_tot += __shfl_xor(l_tot, 32);
+    if (a.n_split > 1) {  // partial of this split, merged by prefill_merge_kernel
+      const int rr = wave * 16 * RB + 16 * r + lq;
+      const int64_t slot = ((((int64_t)b * a.row_blocks + blk) * a.Hkv + kvh) * a.n_split + sp) * ROWS + rr;
+      float* po = a.ws_o + slot * D;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        *(float4*)(po + 16 * nb + 4 * lg) = make_float4(o[r][nb][0], o[r][nb][1], o[r][nb][2], o[r][nb][3]);
+      if (lg == 0) *(float2*)(a.ws_ml + 2 * slot) = make_float2(m_run[r], l_tot);
+      continue;
+    }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (row_ok[r]) {
       uint16_t* orow = a.out + (int64_t)b * a.os_b + (int64_t)head[r] * a.os_h + (int64_t)s[r] * a.os_s;
@@ -358,6 +385,38 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
       }
     }
   }
+}
+
+// Combines the n_split partials of one query row (log-sum-exp in base 2):
+// one workgroup of D threads per (unit, row), thread d owns output dim d.
+template <int D, bool F16>
+__global__ __launch_bounds__(D) void prefill_merge_kernel(const PrefillArgs a, int rows) {
+  const int64_t g = blockIdx.x;
+  const int rr = (int)(g % rows);
+  const int64_t unit = g / rows;  // (b * row_blocks + blk) * Hkv + kvh
+  const int kvh = (int)(unit % a.Hkv);
+  const int64_t t = unit / a.Hkv;
+  const int blk = (int)(t % a.row_blocks);
+  const int b = (int)(t / a.row_blocks);
+  const int R = blk * rows + rr;
+  const int s = R / a.ratio;
+  if (s >= a.Sq) return;
+  const int head = kvh * a.ratio + R % a.ratio;
+  const int d = threadIdx.x;
+  const int64_t slot0 = unit * a.n_split * rows + rr;  // split sp: slot0 + sp * rows
+  float M = kNegP;
+  for (int sp = 0; sp < a.n_split; ++sp) M = fmaxf(M, a.ws_ml[2 * (slot0 + (int64_t)sp * rows)]);
+  float L = 0.0f, acc = 0.0f;
+  for (int sp = 0; sp < a.n_split; ++sp) {
+    const int64_t slot = slot0 + (int64_t)sp * rows;
+    const float2 ml = *(const float2*)(a.ws_ml + 2 * slot);
+    const float w = __builtin_amdgcn_exp2f(ml.x - M);
+    L += ml.y * w;
+    acc += a.ws_o[slot * D + d] * w;
+  }
+  const float v = L > 0.0f ? acc / L : 0.0f;
+  uint16_t* orow = a.out + (int64_t)b * a.os_b + (int64_t)head * a.os_h + (int64_t)s * a.os_s;
+  orow[d] = F16 ? (uint16_t)f32_to_f16_bits(v) : (uint16_t)f32_to_bf16_bits(v);
 }
 
 template <int D, bool F16, int RB>
@@ -375,6 +434,41 @@ template <int D, bool F16>
 void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, dim3 grid, hipStream_t st) {
   if (rb == 2) launch_prefill<D, F16, 2>(a, s_f16, grid, st);
   else launch_prefill<D, F16, 1>(a, s_f16, grid, st);
+  if (a.n_split > 1) {
+    const int rows = kRows * rb;
+    const int64_t n = (int64_t)grid.x / a.n_split * rows;
+    hipLaunchKernelGGL((prefill_merge_kernel<D, F16>), dim3((unsigned)n), dim3(D), 0, st, a, rows);
+  }
+}
+
+// Launch plan: rows per workgroup (rb 16-row blocks per wave), row blocks,
+// and the split over keys. Two row blocks per wave once that still gives
+// 512 or more workgroups (two per CU of a 256-CU device); below 256
+// workgroups, splits of at least 512 keys bring the launch to ~512.
+struct PrefillPlan {
+  int rb, n_split;
+  int64_t row_blocks;
+};
+
+PrefillPlan prefill_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk) {
+  const int64_t ratio = Hq / Hkv;
+  PrefillPlan p;
+  p.rb = B * Hkv * ((Sq * ratio + 2 * kRows - 1) / (2 * kRows)) >= 512 ? 2 : 1;
+  p.row_blocks = (Sq * ratio + p.rb * kRows - 1) / (p.rb * kRows);
+  const int64_t n_wg = B * Hkv * p.row_blocks;
+  int64_t ns = 1;
+  if (p.rb == 1 && n_wg > 0 && n_wg < 256) {
+    ns = (512 + n_wg - 1) / n_wg;
+    ns = std::min<int64_t>(ns, std::max<int64_t>(1, Sk / 512));
+    ns = std::min<int64_t>(ns, 64);
+  }
+  p.n_split = (int)ns;
+  return p;
+}
+
+int64_t prefill_ws_bytes(const PrefillPlan& p, int64_t B, int64_t Hkv, int64_t D) {
+  if (p.n_split <= 1) return 0;
+  return B * Hkv * p.row_blocks * p.n_split * (kRows * p.rb) * (D + 2) * 4;
 }
 
 }  // namespace
@@ -396,7 +490,8 @@ int prefill_impl(const void* q, int q_dtype, const int64_t* q_strides, const voi
                  const void* v_packed, const int64_t* vp_strides, const void* v_scales,
                  const int64_t* vs_strides, int scale_dtype, void* out, const int64_t* out_strides, int64_t B,
                  int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, int64_t group_size, int64_t Sk,
-                 int is_causal, float sm_scale, void* stream, const PrefillPaged* pg) {
+                 int is_causal, float sm_scale, void* workspace, int64_t workspace_bytes, void* stream,
+                 const PrefillPaged* pg) {
   KVQ_CHECK_ARG(q_strides && out_strides, "kvq_prefill_attn: null stride array");
   KVQ_CHECK_ARG(B >= 0 && Hq >= 1 && Hkv >= 1 && Sq >= 0 && Sk >= 0 && Hq % Hkv == 0,
                 "kvq_prefill_attn: bad shape (B=%lld Hq=%lld Hkv=%lld Sq=%lld Sk=%lld)", (long long)B,
@@ -440,11 +535,13 @@ int prefill_impl(const void* q, int q_dtype, const int64_t* q_strides, const voi
   if (B == 0 || Sq == 0) return KVQ_OK;
   KVQ_CHECK_ARG(q && out && (Sk == 0 || (k_packed && k_scales && v_packed && v_scales)),
                 "kvq_prefill_attn: null data pointer");
-  // two 16-row blocks per wave (128 rows per workgroup) once that still
-  // leaves two workgroups per CU of a 256-CU device; one otherwise
-  const int rb = B * Hkv * ((Sq * ratio + 2 * kRows - 1) / (2 * kRows)) >= 512 ? 2 : 1;
-  const int64_t row_blocks = (Sq * ratio + rb * kRows - 1) / (rb * kRows);
-  const int64_t n_wg = B * Hkv * row_blocks;
+  PrefillPlan plan = prefill_plan(B, Hq, Hkv, Sq, Sk);
+  // the split over keys needs the workspace; without one the launch is unsplit
+  const int64_t need = prefill_ws_bytes(plan, B, Hkv, D);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) plan.n_split = 1;
+  const int rb = plan.rb;
+  const int64_t row_blocks = plan.row_blocks;
+  const int64_t n_wg = B * Hkv * row_blocks * plan.n_split;
   KVQ_CHECK_ARG(n_wg < (1ll << 31) && Sq < (1ll << 30) && Sk < (1ll << 30), "kvq_prefill_attn: too large");
 
   PrefillArgs a;
@@ -470,6 +567,9 @@ int prefill_impl(const void* q, int q_dtype, const int64_t* q_strides, const voi
   a.n_blocks = pg ? (int)pg->n_blocks : 0;
   a.page_shift = page_shift;
   if (pg && pg->bt_cols == 0) a.Sk = 0;
+  a.n_split = plan.n_split;
+  a.ws_o = plan.n_split > 1 ? (float*)workspace : nullptr;
+  a.ws_ml = plan.n_split > 1 ? (float*)workspace + B * Hkv * row_blocks * plan.n_split * (kRows * rb) * D : nullptr;
 
   const dim3 grid((unsigned)n_wg);
   hipStream_t st = (hipStream_t)stream;
@@ -496,12 +596,23 @@ extern "C" int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_str
                                 void* out, const int64_t* out_strides,
                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
                                 int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   KVQ_CHECK_ARG(kp_strides && ks_strides && vp_strides && vs_strides, "kvq_prefill_attn: null stride array");
   return prefill_impl(q, q_dtype, q_strides, k_packed, kp_strides, k_scales, ks_strides, v_packed, vp_strides,
                       v_scales, vs_strides, scale_dtype, out, out_strides, B, Hq, Hkv, Sq, D, group_size, Sk,
-                      is_causal, sm_scale, stream, nullptr);
+                      is_causal, sm_scale, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int64_t kvq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                                    int64_t Sk) {
+  clear_error();
+  if (B < 0 || Hq < 1 || Hkv < 1 || Sq < 0 || Sk < 0 || Hq % Hkv != 0 || !(D == 64 || D == 128)) {
+    set_error("kvq_prefill_attn_workspace_bytes: bad shape");
+    return KVQ_EINVAL;
+  }
+  if (B == 0 || Sq == 0) return 0;
+  return prefill_ws_bytes(prefill_plan(B, Hq, Hkv, Sq, Sk), B, Hkv, D);
 }
 
 extern "C" int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,
@@ -515,7 +626,7 @@ extern "C" int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t*
                                       void* out, const int64_t* out_strides,
                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
                                       int64_t group_size, int64_t Sk, int is_causal, float sm_scale,
-                                      void* stream) {
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   KVQ_CHECK_ARG(kp_strides && ks_strides && vp_strides && vs_strides, "kvq_prefill_attn_paged: null stride array");
   const int64_t kp3[3] = {0, kp_strides[0], kp_strides[1]}, ks3[3] = {0, ks_strides[0], ks_strides[1]};
@@ -523,5 +634,5 @@ extern "C" int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t*
   const PrefillPaged pg{block_table, table_stride, table_cols, num_blocks, page_size};
   return prefill_impl(q, q_dtype, q_strides, k_pool, kp3, k_scale_pool, ks3, v_pool, vp3, v_scale_pool, vs3,
                       scale_dtype, out, out_strides, B, Hq, Hkv, Sq, D, group_size, Sk, is_causal, sm_scale,
-                      stream, &pg);
+                      workspace, workspace_bytes, stream, &pg);
 }

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_attn_paged",
     "kvq_decode_step_paged",
     "kvq_prefill_attn",
+    "kvq_prefill_attn_workspace_bytes",
     "kvq_prefill_attn_paged",
 )
 
@@ -92,6 +93,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         _vp, _i64, ctypes.c_float,
         _i64, _vp, _i64, _vp,
     ]
+    lib.kvq_prefill_attn_workspace_bytes.restype = _i64
+    lib.kvq_prefill_attn_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64]
     lib.kvq_prefill_attn.restype = _i32
     lib.kvq_prefill_attn.argtypes = [
         _vp, _i32, _i64p,
@@ -99,7 +102,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i32,
         _vp, _i64p,
         _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-        _i32, ctypes.c_float, _vp,
+        _i32, ctypes.c_float, _vp, _i64, _vp,
     ]
     # paged counterparts: (block_table, table_stride, table_cols, num_blocks,
     # page_size) after the cache arguments; pool strides are (head, row)
@@ -111,7 +114,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i32, *pg,
         _vp, _i64p,
         _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-        _i32, ctypes.c_float, _vp,
+        _i32, ctypes.c_float, _vp, _i64, _vp,
     ]
     lib.kvq_quantize_paged.restype = _i32
     lib.kvq_quantize_paged.argtypes = [

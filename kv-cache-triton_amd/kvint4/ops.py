@@ -28,13 +28,20 @@ SUPPORTED_FLOATS = (torch.bfloat16, torch.float16, torch.float32)
 # faster route up to 1024 rows and flash SDPA beyond 2048, at 512 to 16K keys
 # (e.g. 16K keys, GQA 4: 256 queries 610 vs 652 us, 512 queries 1251 vs 654 us).
 MAX_FUSED_ROWS = 1024
-# Above this many rows per KV head, a block over a contiguous cache with one
-# length for the batch (a prompt, or a prompt chunk after cached tokens) goes
-# to the matrix-core prefill kernel instead (it dequantizes each 64-key tile
-# into LDS once for 64 or 128 rows): 16K keys, GQA 4, 256 queries 499 us vs
-# 614 fused / 664 dequantize + flash; a whole 16K prompt 4.06 ms vs 4.54 ms
-# flash; 128 queries 508 vs 323 fused.
-PREFILL_MIN_ROWS = 512
+# A block of at least PREFILL_MIN_ROWS rows per KV head whose rows x keys
+# reach PREFILL_MIN_WORK, over a cache with one length for the batch (a
+# prompt, a prompt chunk, a large speculative block), goes to the matrix-core
+# prefill kernel instead: it dequantizes each 64-key tile into LDS once for
+# 64 or 128 rows and splits the key range when the launch is small. Measured
+# crossover with the fused kernel (GQA 4): 64 rows at 16K keys (16 queries
+# 48 vs 60 us), 128-256 at 4K, 512-1024 at 1K; a whole 16K prompt takes
+# 3.50 ms vs 4.50 ms for dequantize + flash SDPA.
+PREFILL_MIN_ROWS = 64
+PREFILL_MIN_WORK = 1 << 20
+
+
+def use_prefill_kernel(rows: int, Sk: int) -> bool:
+    return rows >= PREFILL_MIN_ROWS and rows * Sk >= PREFILL_MIN_WORK
 
 
 def dense_fast_path(q: torch.Tensor, seq_lens: torch.Tensor | None) -> bool:
@@ -221,6 +228,20 @@ class _Workspaces:
 
 
 _workspaces = _Workspaces()
+# prefill split partials: a separate buffer, so that they never overwrite the
+# decode kernels' arrival counters
+_prefill_workspaces = _Workspaces()
+
+
+def _prefill_ws(q: torch.Tensor, Hkv: int, Sk: int, stream: int) -> tuple:
+    B, Hq, Sq, D = q.shape
+    n = nat.lib().kvq_prefill_attn_workspace_bytes(B, Hq, Hkv, Sq, D, Sk)
+    if n < 0:
+        nat.check(int(n), "kvq_prefill_attn_workspace_bytes")
+    if n == 0:
+        return None, 0
+    ws = _prefill_workspaces.get(q.device, stream, n)
+    return ws.data_ptr(), ws.numel()
 _cu_count: dict[int, int] = {}
 
 
@@ -337,6 +358,8 @@ def prefill_attention(
         v_scales = v_scales.to(k_scales.dtype)
     lib = nat.lib()
     with nat.device_of(q):
+        stream = nat.stream_handle(q.device)
+        ws_ptr, ws_len = _prefill_ws(q, n_kv_heads, Sk, stream)
         rc = lib.kvq_prefill_attn(
             q.data_ptr(), nat.DTYPE_CODE[q.dtype], nat.i64_array(q.stride()),
             k_packed.data_ptr(), nat.i64_array(k_packed.stride()[:3]),
@@ -346,7 +369,7 @@ def prefill_attention(
             nat.DTYPE_CODE[k_scales.dtype],
             out.data_ptr(), nat.i64_array(out.stride()),
             B, Hq, n_kv_heads, Sq, D, group_size, Sk,
-            1 if is_causal else 0, float(sm_scale), nat.stream_handle(q.device),
+            1 if is_causal else 0, float(sm_scale), ws_ptr, ws_len, stream,
         )
     nat.check(rc, "kvq_prefill_attn")
     return out
@@ -561,7 +584,7 @@ def attention_over_quantized(
     B, Hq, Sq, D = q.shape
     Sk = k_packed.shape[2]
     rows = (Hq // n_kv_heads) * Sq
-    if rows > PREFILL_MIN_ROWS and seq_lens is None:
+    if seq_lens is None and use_prefill_kernel(rows, Sk):
         try:
             return prefill_attention(q, k_packed, k_scales, v_packed, v_scales, n_kv_heads=n_kv_heads,
                                      group_size=group_size, is_causal=is_causal, sm_scale=sm_scale)
@@ -813,6 +836,8 @@ def prefill_attention_paged(
         raise nat.KVQUnsupported("K and V scales must share a dtype")
     lib = nat.lib()
     with nat.device_of(q):
+        stream = nat.stream_handle(q.device)
+        ws_ptr, ws_len = _prefill_ws(q, n_kv_heads, seq_len, stream)
         rc = lib.kvq_prefill_attn_paged(
             q.data_ptr(), nat.DTYPE_CODE[q.dtype], nat.i64_array(q.stride()),
             k_pool.data_ptr(), nat.i64_array(k_pool.stride()[:2]),
@@ -822,7 +847,7 @@ def prefill_attention_paged(
             nat.DTYPE_CODE[k_scales.dtype], *pt.args(),
             out.data_ptr(), nat.i64_array(out.stride()),
             B, Hq, n_kv_heads, Sq, D, group_size, seq_len,
-            1 if is_causal else 0, float(sm_scale), nat.stream_handle(q.device),
+            1 if is_causal else 0, float(sm_scale), ws_ptr, ws_len, stream,
         )
     nat.check(rc, "kvq_prefill_attn_paged")
     return out

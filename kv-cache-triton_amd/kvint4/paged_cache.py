@@ -309,7 +309,7 @@ class PagedQuantizedKVCache:
         S = max(lens, default=0)
         uniform = all(n == S for n in lens)
         dense_fast = ops.dense_fast_path(query_states, None if uniform else seq_lens)
-        if self.page_size >= 64 and uniform and rows > ops.PREFILL_MIN_ROWS:
+        if self.page_size >= 64 and uniform and ops.use_prefill_kernel(rows, S):
             try:
                 return ops.prefill_attention_paged(
                     query_states, *pools, pt, S, n_kv_heads=n_kv_heads, group_size=self.group_size,

@@ -148,12 +148,12 @@ def test_prefill_route_matches_oracle():
 
 @pytest.mark.parametrize("Sq,causal", [(100, True), (100, False), (300, True), (300, False)])
 def test_query_blocks_on_both_routes(Sq, causal):
-    """Blocks of 400 query rows per KV head take the fused decode kernel;
-    1200 rows take the matrix-core prefill kernel. A causal block after
-    cached tokens (a prompt chunk, a speculative block) is aligned
-    bottom-right on both."""
-    Hq, Hkv, Sk = 8, 2, 700
-    assert (Hq // Hkv) * 100 <= ops.PREFILL_MIN_ROWS < (Hq // Hkv) * 300
+    """Over 1000 keys, blocks of 400 query rows per KV head take the fused
+    decode kernel; 1200 rows take the matrix-core prefill kernel. A causal
+    block after cached tokens (a prompt chunk, a speculative block) is
+    aligned bottom-right on both."""
+    Hq, Hkv, Sk = 8, 2, 1000
+    assert not ops.use_prefill_kernel((Hq // Hkv) * 100, Sk) and ops.use_prefill_kernel((Hq // Hkv) * 300, Sk)
     q, kp, ks, vp, vs = _inputs(1, Hq, Hkv, Sq, Sk, 128, "bf16", seed=Sq + causal)
     out = attention_forward_quant_gqa(q.to(DEV), kp, ks, vp, vs, n_q_heads=Hq, n_kv_heads=Hkv, is_causal=causal)
     got = out.float().cpu().numpy()

@@ -372,7 +372,8 @@ def test_paged_attend_small_pages_use_dense_route():
     assert np.abs(out.float().cpu().numpy() - exact).max() <= 2e-2
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,Sq,S,P", [(2, 8, 2, 300, 700, 64), (2, 32, 8, 2048, 2500, 128)])
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,S,P", [(2, 8, 2, 300, 700, 64), (2, 32, 8, 2048, 2500, 128),
+                                             (1, 8, 2, 100, 2000, 64)])
 def test_prefill_kernel_paged_matches_contiguous(B, Hq, Hkv, Sq, S, P):
     """The matrix-core prefill kernel through a block table (one and two row
     blocks per wave) reads the same keys in the same 64-key tiles as on the

@@ -9,7 +9,9 @@ kernel (tests/llama3/test_attention_quant_gqa.py:58-91 uses 5e-2 for its
 prefill case). Cases: a prompt (Sq == Sk), prompt chunks after cached tokens,
 GQA ratios 1/4/8, head dims 64/128, group sizes 32/64/128, fp16, more queries
 than keys (rows with no admissible key are zero), an empty cache, and
-non-contiguous views of a larger cache.
+non-contiguous views of a larger cache. Launches too small to fill the
+device split the key range and merge the splits' partials (log-sum-exp)
+in a second launch; those cases run through that path.
 """
 
 from __future__ import annotations
@@ -53,6 +55,8 @@ CASES = [
     (2, 16, 2, 33, 500, 128, 128, "bf16", True),    # GQA 8, G 128
     (1, 4, 1, 129, 129, 64, 32, "f16", True),       # GQA 4, D 64, a row block cut short
     (1, 8, 2, 200, 150, 128, 32, "bf16", True),     # more queries than keys
+    (1, 8, 2, 100, 3000, 128, 32, "bf16", True),    # split over keys (5 splits), merged
+    (1, 8, 2, 1100, 1100, 128, 32, "bf16", True),   # a prompt split in two: early row blocks leave a split empty
 ]
 
 
