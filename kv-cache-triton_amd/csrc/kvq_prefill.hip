@@ -442,9 +442,9 @@ void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, dim3 grid, hipS
 }
 
 // Launch plan: rows per workgroup (rb 16-row blocks per wave), row blocks,
-// and the split over keys. Two row blocks per wave once that still gives
-// 512 or more workgroups (two per CU of a 256-CU device); below 256
-// workgroups, splits of at least 512 keys bring the launch to ~512.
+// and the split over keys. Two row blocks per wave once that still gives a
+// workgroup per CU of a 256-CU device; below 512 workgroups (two per CU),
+// splits of at least 512 keys bring the launch to ~512.
 struct PrefillPlan {
   int rb, n_split;
   int64_t row_blocks;
@@ -453,11 +453,11 @@ struct PrefillPlan {
 PrefillPlan prefill_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk) {
   const int64_t ratio = Hq / Hkv;
   PrefillPlan p;
-  p.rb = B * Hkv * ((Sq * ratio + 2 * kRows - 1) / (2 * kRows)) >= 512 ? 2 : 1;
+  p.rb = B * Hkv * ((Sq * ratio + 2 * kRows - 1) / (2 * kRows)) >= 256 ? 2 : 1;
   p.row_blocks = (Sq * ratio + p.rb * kRows - 1) / (p.rb * kRows);
   const int64_t n_wg = B * Hkv * p.row_blocks;
   int64_t ns = 1;
-  if (p.rb == 1 && n_wg > 0 && n_wg < 256) {
+  if (n_wg > 0 && n_wg < 512) {
     ns = (512 + n_wg - 1) / n_wg;
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, Sk / 512));
     ns = std::min<int64_t>(ns, 64);

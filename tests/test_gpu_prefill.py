@@ -91,13 +91,15 @@ def test_prefill_empty_cache_and_unsupported():
         ops.prefill_attention(q32, kp, ks, kp, ks, n_kv_heads=2, group_size=32, is_causal=True, sm_scale=0.1)
 
 
-def test_prefill_two_row_blocks_per_wave():
-    """A launch of >= 512 workgroups takes two 16-row blocks per wave (128
-    rows per workgroup): the whole output against the dense route, and rows
-    across the block against the fp64 oracle (row i of a causal block after
-    cached tokens attends keys [0, Sk - Sq + i])."""
-    B, Hq, Hkv, Sq, Sk, D, G = 2, 32, 8, 1024, 3000, 128, 32
-    assert B * Hkv * (Sq * (Hq // Hkv) // 128) >= 512
+@pytest.mark.parametrize("B", [1, 2])
+def test_prefill_two_row_blocks_per_wave(B):
+    """Launches of >= 256 workgroups of 128 rows take two 16-row blocks per
+    wave (B = 2: 512 of them, unsplit; B = 1: 256, split in two over keys):
+    the whole output against the dense route, and rows across the block
+    against the fp64 oracle (row i of a causal block after cached tokens
+    attends keys [0, Sk - Sq + i])."""
+    Hq, Hkv, Sq, Sk, D, G = 32, 8, 1024, 3000, 128, 32
+    assert B * Hkv * (Sq * (Hq // Hkv) // 128) >= 256
     q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, "bf16", G, seed=11)
     out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=True,
                                 sm_scale=D ** -0.5)
