@@ -105,3 +105,44 @@ def test_check_maps_status_to_exceptions():
         nat.check(nat.KVQ_EUNSUP, "x")
     with pytest.raises(RuntimeError):
         nat.check(nat.KVQ_EHIP, "x")
+
+
+def test_prefill_entry_points_validate_before_any_launch():
+    """kvq_prefill_attn(_paged): shape, dtype and geometry checks, and the
+    split plan's workspace figures, all host arithmetic (no device call)."""
+    lib = nat.lib()
+    B16, F32 = nat.KVQ_BF16, nat.KVQ_F32
+    q4 = nat.i64_array([32 * 64 * 128, 64 * 128, 128, 1])
+    c3 = nat.i64_array([8 * 1000 * 64, 1000 * 64, 64])
+    s3 = nat.i64_array([8 * 1000 * 4, 1000 * 4, 4])
+
+    def call(q_dtype=B16, s_dtype=B16, B=1, Hq=32, Hkv=8, Sq=64, D=128, G=32, Sk=1000, q_str=q4):
+        return lib.kvq_prefill_attn(None, q_dtype, q_str, None, c3, None, s3, None, c3, None, s3, s_dtype,
+                                    None, q4, B, Hq, Hkv, Sq, D, G, Sk, 1, 0.1, None, 0, None)
+
+    assert call(Hq=30) == nat.KVQ_EINVAL                      # Hq not a multiple of Hkv
+    assert call(q_dtype=F32) == nat.KVQ_EUNSUP and "bf16/fp16" in nat.last_error()
+    assert call(D=96) == nat.KVQ_EUNSUP
+    assert call(Hq=8 * 5) == nat.KVQ_EUNSUP                   # GQA ratio 5 does not divide 64
+    assert call(q_str=nat.i64_array([0, 0, 256, 2])) == nat.KVQ_EUNSUP and "contiguous" in nat.last_error()
+    assert call(B=0) == nat.KVQ_OK and call(Sq=0) == nat.KVQ_OK    # nothing to launch, no pointer read
+    assert call() == nat.KVQ_EINVAL and "null" in nat.last_error()
+    # paged: page size and table geometry
+    p2 = nat.i64_array([4096 * 64, 64])
+    p2s = nat.i64_array([4096 * 4, 4])
+
+    def paged(page_size=64, cols=16, n_blocks=64, Sk=1000):
+        return lib.kvq_prefill_attn_paged(None, B16, q4, None, p2, None, p2s, None, p2, None, p2s, B16,
+                                          None, 16, cols, n_blocks, page_size, None, q4,
+                                          1, 32, 8, 64, 128, 32, Sk, 1, 0.1, None, 0, None)
+
+    assert paged(page_size=32) == nat.KVQ_EINVAL and "page_size" in nat.last_error()
+    assert paged(Sk=16 * 64 + 1) == nat.KVQ_EINVAL            # Sk past the table's capacity
+    assert paged() == nat.KVQ_EINVAL and "null" in nat.last_error()
+    # split plan: a launch too small for the device splits over keys and needs
+    # (D + 2) floats per row, split and workgroup; one that fills it needs none
+    ws = lib.kvq_prefill_attn_workspace_bytes(1, 32, 8, 128, 128, 16384)
+    assert ws == 8 * 8 * 8 * 64 * (128 + 2) * 4              # 8 heads x 8 row blocks x 8 splits x 64 rows
+    assert lib.kvq_prefill_attn_workspace_bytes(1, 32, 8, 16384, 128, 16384) == 0
+    assert lib.kvq_prefill_attn_workspace_bytes(0, 32, 8, 128, 128, 16384) == 0
+    assert lib.kvq_prefill_attn_workspace_bytes(1, 32, 8, 128, 96, 16384) == nat.KVQ_EINVAL
