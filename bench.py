@@ -87,6 +87,9 @@ def main() -> int:
     ap.add_argument("--prefill", type=int, default=0, metavar="SQ",
                     help="time the matrix-core prefill kernel instead: a causal block of SQ query tokens "
                          "over the workload's context (SQ == --ctx: a whole prompt), one JSON line")
+    ap.add_argument("--model", action="store_true",
+                    help="whole-model decode instead: random-init Llama-3.1-8B (C3), 16K prompt, 64 greedy "
+                         "steps over the INT4 cache, each step one HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -127,6 +130,8 @@ def main() -> int:
         w["ctx"] = args.ctx
     if args.prefill:
         return prefill_bench(args, w)
+    if args.model:
+        return model_bench(args)
     B, Hq, Hkv, D, G, ctx, L = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"], w["layers"]
     tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w["dtype"]]
     sdt = torch.float16 if w["dtype"] != "bf16" else torch.bfloat16  # GPT-2: fp16 scales
@@ -425,6 +430,97 @@ def prefill_bench(args, w: dict) -> int:
         "roofline": {"bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
                      "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4), "traffic": None, "kernel": "prefill_attn_kernel"},
         "dequant_flash_ms_per_layer": round(ms_dense, 4), "max_abs_vs_dequant_flash": err,
+    }), flush=True)
+    return 0
+
+
+def model_bench(args) -> int:
+    """Whole-model decode at the C3 configuration: random-init Llama-3.1-8B in
+    bf16 (weights ~N(0, 0.02) from the HF initialiser, seed 2), a 16384-token
+    uniform random prompt (seed 2), prefill through the swapped attention
+    modules (INT4 cache, matrix-core prefill kernel), then 64 greedy steps:
+    2 eager warmup steps, then one HIP graph replay per token
+    (kvint4.llama3.graph_decode). ms/token is the replays' event time over
+    their count. Eager HF decoding of the same cache is timed beside it. The
+    roofline is that of the whole step: every weight but the embedding table is
+    read once per token (bf16 GEMV), plus each layer's INT4 K/V."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from kvint4.llama3.graph_decode import GraphedGreedyDecoder
+    from kvint4.llama3.kv_cache import QuantizedKVCache
+    from kvint4.llama3.llama3_quant import replace_llama_attention_with_quantized
+
+    prompt_len, total, warm, eager_steps = 16384, 64, 2, 8
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                      num_attention_heads=32, num_key_value_heads=8, rope_theta=500000.0,
+                      max_position_embeddings=131072, rms_norm_eps=1e-5, initializer_range=0.02,
+                      tie_word_embeddings=False)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    torch.manual_seed(2)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    model.set_attn_implementation("sdpa")
+    replace_llama_attention_with_quantized(model, group_size=32)
+    print("bench.py --model: model initialised", file=sys.stderr, flush=True)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(2)).to(dev)
+    cache = QuantizedKVCache(group_size=32, reserve_tokens=prompt_len + total + eager_steps + 64)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+        del out
+        # eager HF decoding of the same cache (Python overhead included)
+        eager = []
+        for _ in range(eager_steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = model(input_ids=nxt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            eager.append(time.perf_counter() - t0)
+    print(f"bench.py --model: prefill {prefill_s:.2f} s, eager decode done", file=sys.stderr, flush=True)
+    dec = GraphedGreedyDecoder(model, cache, nxt, max_new_tokens=total, warmup_steps=warm)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    toks = dec.run()
+    e1.record()
+    torch.cuda.synchronize()
+    replays = total - warm
+    ms_tok = e0.elapsed_time(e1) / replays
+    kv_tokens = cache.get_seq_length(0)
+    assert kv_tokens == prompt_len + eager_steps + total, kv_tokens
+    weight_bytes = sum(p.numel() * p.element_size() for n, p in model.named_parameters() if "embed_tokens" not in n)
+    w = WORKLOADS["ns"]
+    mid = prompt_len + eager_steps + (warm + total) // 2  # keys attended by the middle replay
+    kv_bytes = cfg.num_hidden_layers * (attn_bytes(w, mid) + append_bytes(w))
+    gbs = (weight_bytes + kv_bytes) / (ms_tok * 1e-3) / 1e9
+    eager_ms = 1e3 * sorted(eager)[len(eager) // 2]
+    print(json.dumps({
+        "metric": "Llama-3.1-8B decode ms/token, INT4 KV cache, 16K prompt", "value": round(ms_tok, 4),
+        "unit": "ms/token", "n_gpus": 1, "steps": replays, "warmup": warm, "ms_per_step": round(ms_tok, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights ~N(0,0.02), seed 2; uniform random 16384-token prompt, seed 2)",
+        "config": {"workload": "llama3.1-8b-c3-prefill16k-greedy64", "batch": 1, "layers": 32, "hidden": 4096,
+                   "q_heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256, "group_size": 32,
+                   "prompt": prompt_len, "graph": True},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole decode step (bf16 weights once + INT4 K/V of every layer)",
+                     "bytes_per_step": int(weight_bytes + kv_bytes)},
+        "eager_hf_ms_per_token": round(eager_ms, 3), "prefill_s": round(prefill_s, 3),
+        "kv_cache_mib": round(cache.nbytes() / 2**20, 2),
+        "tokens_head": toks[0, :8].tolist(),
     }), flush=True)
     return 0
 

@@ -34,7 +34,8 @@ _ROUND = 256  # capacity granularity (tokens)
 class _LayerQuantizedKV:
     """Per-layer state. Field names follow the reference
     (models/llama3/kv_cache.py:21-27); the tensors may hold more rows than
-    ``seq_len`` (capacity). ``seq_lens`` is set only for ragged layers."""
+    ``seq_len`` (capacity). ``seq_lens`` (device lengths) is set for ragged
+    layers and after ``make_static``."""
 
     k_packed: torch.Tensor
     k_scales: torch.Tensor
@@ -62,6 +63,7 @@ class QuantizedKVCacheBase:
         self.group_size = int(group_size)
         self.reserve_tokens = int(reserve_tokens)
         self._layers: dict[int, _LayerQuantizedKV] = {}
+        self.fused_steps = 0  # append_and_attend calls served by the one-launch decode step
 
     # -- family policy -------------------------------------------------------
     def _scale_dtype_for(self, x: torch.Tensor) -> torch.dtype:  # pragma: no cover
@@ -125,13 +127,58 @@ class QuantizedKVCacheBase:
         if layer.k_scales.dtype != scale_dtype:
             raise ValueError(f"layer {layer_idx}: scale dtype {scale_dtype} differs from the cache's")
         if needed > layer.capacity:
-            cap = _round_up(max(needed, 2 * layer.capacity), _ROUND)
-            kp, ks, vp, vs = self._alloc(key_states, B, H, cap, D, scale_dtype)
-            n = layer.seq_len
-            for dst, src in ((kp, layer.k_packed), (ks, layer.k_scales), (vp, layer.v_packed), (vs, layer.v_scales)):
-                dst[:, :, :n].copy_(src[:, :, :n])
-            layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales = kp, ks, vp, vs
+            self._grow(layer, _round_up(max(needed, 2 * layer.capacity), _ROUND))
         return layer
+
+    @staticmethod
+    def _grow(layer: _LayerQuantizedKV, cap: int) -> None:
+        """Move a layer's rows into buffers of `cap` rows (one copy)."""
+        n = layer.seq_len
+        new = [torch.empty((*t.shape[:2], cap, t.shape[3]), dtype=t.dtype, device=t.device)
+               for t in (layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales)]
+        for dst, src in zip(new, (layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales)):
+            dst[:, :, :n].copy_(src[:, :, :n])
+        layer.k_packed, layer.k_scales, layer.v_packed, layer.v_scales = new
+
+    def make_static(self, extra_tokens: int) -> None:
+        """Prepare every layer for decode steps captured in a HIP graph.
+
+        A replay cannot allocate, and it must not bake a Python write position
+        into its launches. So room for `extra_tokens` more tokens per sequence
+        is reserved now, and each layer's lengths move to a device int32 [B]
+        tensor (if not there already, as for ragged layers). ``append`` and
+        ``append_and_attend`` then read the write position from that tensor and
+        advance it in place, which a captured step replays.
+
+        The Python-side lengths (``get_seq_length``) are not touched by a replay.
+        Whoever replays advances them with ``advance_host_lengths``."""
+        extra_tokens = int(extra_tokens)
+        if extra_tokens < 0:
+            raise ValueError("extra_tokens must be >= 0")
+        if not self._layers:
+            raise ValueError("make_static needs a prefilled cache (no layer holds tokens)")
+        for layer in self._layers.values():
+            need = layer.seq_len + extra_tokens
+            if need > layer.capacity:
+                self._grow(layer, _round_up(need, _ROUND))
+            if layer.seq_lens is None:
+                B = int(layer.k_packed.shape[0])
+                layer.seq_lens = torch.full((B,), layer.seq_len, dtype=torch.int32, device=layer.k_packed.device)
+
+    def room(self) -> int:
+        """Tokens every layer can still take without growing its buffers."""
+        return min((l.capacity - l.seq_len for l in self._layers.values()), default=0)
+
+    def host_lengths(self) -> dict[int, int]:
+        """Python-side length of every layer (what ``get_seq_length`` reports)."""
+        return {i: int(l.seq_len) for i, l in self._layers.items()}
+
+    def advance_host_lengths(self, base: dict[int, int], n: int) -> None:
+        """Set each layer's Python-side length to base[layer] + n: the
+        bookkeeping of n decode steps that ran as graph replays (the device
+        lengths were advanced by the replays themselves)."""
+        for i, l in self._layers.items():
+            l.seq_len = int(base[i]) + int(n)
 
     def _append_quantized(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> None:
         if key_states.shape != value_states.shape:
@@ -192,6 +239,7 @@ class QuantizedKVCacheBase:
         if layer.seq_lens is not None:
             layer.seq_lens.add_(1)
         layer.seq_len = start + 1
+        self.fused_steps += 1
         return out
 
     def load_ragged(

@@ -170,3 +170,42 @@ def test_cpu_tensors_are_rejected_by_the_product_path():
         ops.quantize(torch.randn(2, 64), 32, torch.float32)
     with pytest.raises(ValueError):
         cache_base.QuantizedKVCacheBase(group_size=-1)
+
+
+def test_make_static_reserves_room_and_moves_lengths_to_device_tensors():
+    c = QuantizedKVCache()
+    with pytest.raises(ValueError):
+        c.make_static(4)
+    for i, n in ((0, 5), (1, 5)):
+        c._layers[i] = _LayerQuantizedKV(
+            k_packed=torch.arange(2 * 2 * 8 * 4, dtype=torch.uint8).view(2, 2, 8, 4),
+            k_scales=torch.ones(2, 2, 8, 1, dtype=torch.bfloat16),
+            v_packed=torch.full((2, 2, 8, 4), 7, dtype=torch.uint8),
+            v_scales=torch.ones(2, 2, 8, 1, dtype=torch.bfloat16), seq_len=n)
+    before = c.get_quantized(0)
+    before = [t.clone() for t in before]
+    assert c.room() == 3
+    c.make_static(300)
+    assert c.room() >= 300 and c._layers[0].capacity % 256 == 0
+    for a, b in zip(before, c.get_quantized(0)):  # the stored rows moved with the growth
+        assert torch.equal(a, b)
+    assert c.get_seq_lens(1).dtype == torch.int32 and c.get_seq_lens(1).tolist() == [5, 5]
+    base = c.host_lengths()
+    c.advance_host_lengths(base, 3)
+    assert c.get_seq_length(0) == 8 and c.get_seq_length(1) == 8
+    with pytest.raises(ValueError):
+        c.make_static(-1)
+
+
+def test_graph_decoder_rejects_unswapped_models_and_other_caches():
+    from kvint4.llama3.graph_decode import GraphedGreedyDecoder
+    from kvint4.paged_cache import PagedQuantizedKVCache
+
+    cfg = LlamaConfig(vocab_size=64, hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                      num_attention_heads=2, num_key_value_heads=1)
+    model = LlamaForCausalLM(cfg)
+    tok = torch.zeros(1, 1, dtype=torch.int64)
+    with pytest.raises(ValueError, match="replace_llama_attention_with_quantized"):
+        GraphedGreedyDecoder(model, QuantizedKVCache(), tok, max_new_tokens=4)
+    with pytest.raises(TypeError):
+        GraphedGreedyDecoder(model, PagedQuantizedKVCache(), tok, max_new_tokens=4)
