@@ -171,3 +171,62 @@ def test_decode_step_in_hip_graph_replays():
         assert torch.equal(out, want)
         for x, y in zip(a, cache_want):
             assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("D,n_split", [(64, None), (128, None), (128, 1)])
+def test_decode_steps_of_several_layers_in_one_graph_advance_device_positions(D, n_split):
+    """Four layers' decode steps captured in one HIP graph, each advancing its
+    layer's device positions in place (the shape of a captured model step and
+    of the bench's timed step), replayed with new inputs copied in between:
+    every replay's outputs and the caches equal the same launches made
+    eagerly, bit for bit."""
+    print(f"graph of 4 decode steps: D {D}, n_split {n_split}", flush=True)
+    B, Hq, Hkv, G, cap, fill, steps, nl = 2, 8, 2, 32, 512, 70, 6, 4
+    sm = D ** -0.5
+    g = torch.Generator(device=DEV).manual_seed(30 + D)
+    caches_e = [_cache(B, Hkv, cap, D, G, "bf16", fill, seed=40 + l) for l in range(nl)]
+    caches_g = [_cache(B, Hkv, cap, D, G, "bf16", fill, seed=40 + l) for l in range(nl)]
+    inp = [[tuple(torch.randn(B, h, 1, D, device=DEV, generator=g).to(torch.bfloat16) for h in (Hq, Hkv, Hkv))
+            for _ in range(nl)] for _ in range(steps)]
+    kw = dict(n_kv_heads=Hkv, group_size=G, sm_scale=sm, n_split=n_split)
+    pos_e = [torch.full((B,), fill, dtype=torch.int32, device=DEV) for _ in range(nl)]
+    eager = []
+    for i in range(steps):
+        row = []
+        for l in range(nl):
+            row.append(ops.decode_step(*inp[i][l], *caches_e[l], pos_e[l], **kw).clone())
+            pos_e[l].add_(1)
+        eager.append(row)
+    pos_g = [torch.full((B,), fill, dtype=torch.int32, device=DEV) for _ in range(nl)]
+    static = [tuple(t.clone() for t in inp[0][l]) for l in range(nl)]
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    first = []
+    with torch.cuda.stream(side):  # step 0 eagerly on the capture stream (its workspace)
+        for l in range(nl):
+            first.append(ops.decode_step(*static[l], *caches_g[l], pos_g[l], **kw).clone())
+            pos_g[l].add_(1)
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = []
+        for l in range(nl):
+            outs.append(ops.decode_step(*static[l], *caches_g[l], pos_g[l], **kw))
+            pos_g[l].add_(1)
+    got = [first]
+    junk = torch.randn(256, 256, device=DEV)
+    for i in range(1, steps):
+        for l in range(nl):
+            for dst, src in zip(static[l], inp[i][l]):
+                dst.copy_(src)
+        graph.replay()
+        junk = (junk @ junk).tanh_()
+        torch.cuda.synchronize()
+        got.append([o.clone() for o in outs])
+    for i in range(steps):
+        for l in range(nl):
+            assert torch.equal(got[i][l], eager[i][l]), (i, l)
+    for l in range(nl):
+        assert torch.equal(pos_g[l], pos_e[l])
+        for a, b in zip(caches_e[l], caches_g[l]):
+            assert torch.equal(a, b)
