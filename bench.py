@@ -91,7 +91,8 @@ def main() -> int:
                     help="whole-model decode instead: random-init Llama-3.1-8B (C3), 16K prompt, 64 greedy "
                          "steps over the INT4 cache, each step one HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="wall budget of the CPU sample")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="wall budget of the CPU sample (the torch path; the C restatement gets a quarter)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run a plain device copy of this many MiB (the "
                          "calibration kernel for rocprof FETCH_SIZE / WRITE_SIZE)")
@@ -610,49 +611,90 @@ def read_traffic(path: str, w: dict):
     return None
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(w: dict, layers: list, attended: int, seq_lens, budget_s: float) -> dict:
-    """Time the C restatement of the reference's CPU path (dequantize + SDPA
-    over the INT4 cache, plus the quantize-append) on the host cores, on as
-    many layers of the same workload as fit in `budget_s` seconds."""
+    """Time the reference's PyTorch CPU path on the host cores: per layer-step,
+    quantize the new K/V row, torch.cat the four tensors onto that layer's cache
+    (models/llama3/kv_cache.py:96-101), dequantize the whole cache and attend
+    with repeat_interleave + SDPA (oracle/kvq_torch.py restates each step). The
+    sample rotates over every layer of the workload (each with its own cache,
+    copied from the GPU), as the GPU step does, for about `budget_s` seconds,
+    with torch's intra-op thread count (OMP_NUM_THREADS, the process's CPU
+    share). The C restatement (oracle/kvq_ref.c, OpenMP, no concatenation) is
+    timed beside it on a shorter sample and reported as `c_port`."""
     import numpy as np
+    import torch
 
     from oracle import kvq_ref as R
+    from oracle import kvq_torch as T
 
     B, Hq, Hkv, D, G = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"]
-    threads = R.num_threads()
-    sample = layers[: max(1, min(len(layers), 4))]
-    host = []
-    for layer in sample:
-        n = attended
-        host.append(dict(
-            kp=layer["kp"][:, :, :n].cpu().numpy(), vp=layer["vp"][:, :, :n].cpu().numpy(),
-            ks=layer["ks"][:, :, :n].float().cpu().numpy(), vs=layer["vs"][:, :, :n].float().cpu().numpy(),
-            q=layer["q"].float().cpu().numpy(), knew=layer["knew"].float().cpu().numpy(),
-            vnew=layer["vnew"].float().cpu().numpy(),
-        ))
-    sl = None if seq_lens is None else (seq_lens + 1).cpu().numpy()
-    sdt = "bf16" if w["dtype"] == "bf16" else "f16"
+    n = attended - 1  # cached rows before the step's append
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w["dtype"]]
+    caches, steps_in = [], []
+    for layer in layers:
+        kp, ks, vp, vs = (layer[k][:, :, :n].cpu().contiguous() for k in ("kp", "ks", "vp", "vs"))
+        caches.append(T.LayerCache(kp, ks, vp, vs, G))
+        steps_in.append((layer["q"].cpu(), layer["knew"].cpu(), layer["vnew"].cpu()))
+    scale = D ** -0.5
+    threads = torch.get_num_threads()
+    T.decode_step(caches[0], *steps_in[0], scale)  # warm up the operators once
     done, t0 = 0, time.perf_counter()
     while True:
-        h = host[done % len(host)]
-        R.quantize_int4(h["knew"], G, sdt)
-        R.quantize_int4(h["vnew"], G, sdt)
-        R.decode_attn(h["q"], h["kp"], h["ks"], h["vp"], h["vs"], group_size=G, scale=D ** -0.5,
-                      seq_lens=sl, threads=threads)
+        i = done % len(caches)
+        c = caches[i]
+        if c.kp.shape[2] > n + 64:  # keep each layer near the workload's context
+            c.kp, c.ks, c.vp, c.vs = c.kp[:, :, :n].clone(), c.ks[:, :, :n].clone(), c.vp[:, :, :n].clone(), c.vs[:, :, :n].clone()
+        T.decode_step(c, *steps_in[i], scale)
         done += 1
-        if time.perf_counter() - t0 > budget_s and done >= 2:
+        if time.perf_counter() - t0 > budget_s and done >= max(2, len(caches)):  # every layer at least once
             break
     dt = time.perf_counter() - t0
-    kv_tokens = int(sl.sum()) if sl is not None else B * attended
+    kv_tokens = int((seq_lens + 1).sum()) if seq_lens is not None else B * attended
     per = attn_bytes(w, kv_tokens) + append_bytes(w)
+
+    # the C restatement on a shorter sample of the same layers
+    c_threads = R.num_threads()
+    sdt = "bf16" if w["dtype"] == "bf16" else "f16"
+    sl = None if seq_lens is None else (seq_lens + 1).cpu().numpy()
+    c_done, c_t0, c_budget = 0, time.perf_counter(), max(1.0, budget_s / 4)
+    while True:
+        c = caches[c_done % len(caches)]
+        q, kn, vn = (x.float().numpy() for x in steps_in[c_done % len(caches)])
+        R.quantize_int4(kn, G, sdt)
+        R.quantize_int4(vn, G, sdt)
+        R.decode_attn(q, c.kp.numpy(), c.ks.float().numpy(), c.vp.numpy(), c.vs.float().numpy(), group_size=G,
+                      scale=scale, seq_lens=sl, threads=c_threads)
+        c_done += 1
+        if time.perf_counter() - c_t0 > c_budget and c_done >= 2:
+            break
+    c_dt = time.perf_counter() - c_t0
     return {
         "value": round(done * per / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{done} layer-steps ({w['desc']}, {len(host)} distinct layers cycled), "
-                  f"C restatement oracle/kvq_ref.c, OpenMP x{threads}, {dt:.1f} s",
+        "sample": f"{done} layer-steps of {w['desc']} over its {len(caches)} layers (each its own cache, "
+                  f"{len(caches) * per / 2**20:.0f} MiB), the reference's torch CPU path (quantize, torch.cat "
+                  f"append, dequantize, repeat_interleave + SDPA; oracle/kvq_torch.py), {threads} torch threads, "
+                  f"{dt:.1f} s",
         "ms_per_layer": round(dt / done * 1e3, 3),
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "c_port": {"value": round(c_done * per / c_dt / 1e9, 3), "unit": "GB/s", "cores": c_threads,
+                   "ms_per_layer": round(c_dt / c_done * 1e3, 3),
+                   "sample": f"{c_done} layer-steps, oracle/kvq_ref.c (OpenMP, no concatenation), {c_dt:.1f} s"},
     }
 
 

@@ -13,9 +13,10 @@
 // balanced to the token (split s of a sequence of L keys covers
 // [s*L/n_split, (s+1)*L/n_split)), so ragged batches stay balanced too. Partial
 // (max, sum, o) triples are merged across the waves of a workgroup in LDS and
-// then across splits by the last workgroup of the unit to finish (partials
-// stored and loaded with the device-coherent sc1 policy, arrival counted by
-// atomics), which writes the output and re-arms the counters. In a decode step
+// then across splits by the last workgroup of the unit to finish (all splits of
+// a unit run on one XCD, so the partials go through that XCD's L2; arrivals
+// are counted by a device-scope atomic), which writes the output and re-arms
+// the counter. In a decode step
 // the same launch also quantizes the new token's K/V into the cache row after
 // the last one, and the unit's last split attends it from registers.
 //
@@ -44,6 +45,7 @@
 //   fp16: (1024+n) - 1032 = n - 8 exactly (v_pk_add_f16), no correction.
 // Softmax runs in base 2 with sm_scale*log2(e) folded into the key scale.
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "kvq_common.h"
@@ -65,8 +67,16 @@ struct AttnArgs {
   int64_t os_b, os_h, os_s, os_d;
   const int32_t* seq_lens;
   int Hkv, Sq, G, Sk, ratio, rows_total, row_chunks, n_units;
-  int n_split, causal, scale_dtype, xcd_remap, q_vec;
+  int n_split, causal, scale_dtype, q_vec, out_vec;
+  int grid_y;  // the launch's gridDim.y (read from here: the dispatch's own copy
+               // would be one more scalar load round trip in the prologue)
   float scale_log2;
+  // launch constants computed on the host, so that the prologue (which every
+  // wave runs before it can issue a load) has no divide: unit = (b * Hkv + kvh)
+  // * row_chunks + rc, query row rho = (head - kvh * ratio) * Sq + qi
+  FastDiv div_rc, div_hkv, div_sq, div_g, div_ns;
+  int ng;             // scales per token row, ceil(D / G)
+  uint32_t gsh_pack;  // byte c: bit offset of 32-dim chunk c's scale in a token's scale row
   // decode step (append != 0): the new token's K/V rows [B, Hkv, 1, D] (q's
   // dtype, unit inner stride), quantized and written at each sequence's old
   // length (seq_lens[b], or pos0 for all) and attended along with the cache
@@ -83,8 +93,8 @@ struct AttnArgs {
   int64_t bt_stride;
   int bt_cols, n_blocks, page_shift;
   uint32_t pool_rows;
-  uint32_t* ws_cnt;  // [kCntUnits][kSubCnt + 1] arrival counters, kCntStride
-                     // words apart (zero between calls)
+  uint32_t* ws_cnt;  // [kCntUnits] arrival counters, kCntStride words apart
+                     // (zero between calls)
   float* ws_ml;      // [n_units][n_split][ROWS][2]  (max, sum)
   float* ws_o;       // [n_units][n_split][ROWS][D]
 };
@@ -92,7 +102,6 @@ struct AttnArgs {
 constexpr float kNeg = -1.0e30f;
 constexpr int kMaxSplit = 64;  // split-K fan-out cap (bounds the merge's LDS)
 constexpr float kLazyMax = 8.0f;  // running-max slack of the MFMA kernel (log2 units)
-constexpr int kSubCnt = 4;      // arrival sub-counters per unit
 constexpr int kCntStride = 16;  // uint32 words between counters (64 bytes)
 constexpr uint32_t kNibPairs = 0x000F000Fu;
 constexpr uint32_t kBf16Magic = 0x43004300u;  // bf16(128), bf16(128)
@@ -189,41 +198,95 @@ __device__ __forceinline__ float load_scale(const char* base, uint32_t off, int 
   return scale16_to_f32(((const uint16_t*)base)[off], dt == KVQ_F16);
 }
 
-// Workgroup -> (unit, split). With XCD remapping all splits of one unit run on
-// the same XCD (workgroups are dealt to the 8 XCDs round-robin), so the split
-// merge reads partials written through the same L2.
-__device__ __forceinline__ void unit_and_split(const AttnArgs& a, int& unit, int& split) {
-  const int j = blockIdx.x;
-  if (a.xcd_remap) {
-    const int xcd = j & 7, local = j >> 3;
-    unit = xcd + 8 * (local / a.n_split);
-    split = local % a.n_split;
-  } else {
-    unit = j / a.n_split;
-    split = j % a.n_split;
-  }
+// Workgroup -> (unit, split). The grid is (8 * n_split, Y, Z) with Y Z >=
+// ceil(n_units / 8): split = x / 8, unit = x % 8 + 8 (y + Y z); workgroups of
+// units past the last exit at once. The hardware deals the workgroups of a
+// launch to the 8 XCDs round-robin in launch order (linear index
+// x + X (y + Y z), from an XCD that varies per launch), and X = 8 n_split is a
+// multiple of 8, so all splits of a unit share x % 8 and run on one XCD, whose
+// L2 then carries the unit's partials.
+__device__ __forceinline__ bool unit_and_split(const AttnArgs& a, int& unit, int& split) {
+  split = (int)(blockIdx.x >> 3);
+  unit = (int)((blockIdx.x & 7u) + 8u * (blockIdx.y + (uint32_t)a.grid_y * blockIdx.z));
+  return unit < a.n_units;
+}
+
+// (b, kvh, rc) of a unit.
+__device__ __forceinline__ void unit_coords(const AttnArgs& a, int unit, int& b, int& kvh, int& rc) {
+  const uint32_t bh = fdiv((uint32_t)unit, a.div_rc);
+  rc = unit - (int)bh * a.row_chunks;
+  b = (int)fdiv(bh, a.div_hkv);
+  kvh = (int)bh - b * a.Hkv;
 }
 
 __device__ __forceinline__ int64_t out_index(const AttnArgs& a, int b, int kvh, int rho, int d) {
-  const int head = kvh * a.ratio + rho / a.Sq, qi = rho % a.Sq;
+  const int hq = (int)fdiv((uint32_t)rho, a.div_sq), qi = rho - hq * a.Sq;
+  const int head = kvh * a.ratio + hq;
   return (int64_t)b * a.os_b + (int64_t)head * a.os_h + (int64_t)qi * a.os_s + (int64_t)d * a.os_d;
 }
 
-// Token range [t0, t1) of split `split` over a sequence of L keys.
-// 32-bit arithmetic: the host keeps Sk * kMaxSplit below 2^32.
+// Four consecutive output elements (dims d .. d + 3 of one row) from element
+// index i: one 8-byte (16-bit types) or 16-byte (fp32) store when the host
+// found the output's dims contiguous and every row aligned for it (out_vec),
+// else four element stores.
+__device__ __forceinline__ void store4_from_f32(const AttnArgs& a, int64_t i, int dt, float x, float y, float z,
+                                                float w) {
+  if (a.out_vec) {
+    if (dt == KVQ_F32) {
+      *(float4*)((float*)a.out + i) = make_float4(x, y, z, w);
+    } else {
+      const bool h = dt == KVQ_F16;
+      const uint32_t e0 = h ? f32_to_f16_bits(x) : f32_to_bf16_bits(x), e1 = h ? f32_to_f16_bits(y) : f32_to_bf16_bits(y);
+      const uint32_t e2 = h ? f32_to_f16_bits(z) : f32_to_bf16_bits(z), e3 = h ? f32_to_f16_bits(w) : f32_to_bf16_bits(w);
+      *(uint2*)((uint16_t*)a.out + i) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+    }
+    return;
+  }
+  store_from_f32(a.out, i, dt, x);
+  store_from_f32(a.out, i + a.os_d, dt, y);
+  store_from_f32(a.out, i + 2 * a.os_d, dt, z);
+  store_from_f32(a.out, i + 3 * a.os_d, dt, w);
+}
+
+__device__ __forceinline__ int div_splits(const AttnArgs& a, uint32_t n) { return (int)fdiv(n, a.div_ns); }
+
+// Element b of a device int32 array that no kernel of this launch writes,
+// read through the scalar cache (a constant-address-space load with a
+// wave-uniform address is a scalar load, counted apart from the vector
+// loads, so waiting for it does not wait for the query and cache loads).
+__device__ __forceinline__ int load_const_i32(const int32_t* p, int i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
+// The kernel arguments the prologue of the decode kernels reads, fetched
+// before their first use. Without this the compiler issues the scalar loads of
+// the argument block in several batches, one per branch of the prologue, and
+// each batch is a round trip before the next one can start.
+__device__ __forceinline__ void fetch_prologue_args(const AttnArgs& a) {
+  asm volatile("" ::"s"(a.n_units), "s"(a.grid_y), "s"(a.div_rc.m), "s"(a.div_rc.s), "s"(a.row_chunks), "s"(a.div_hkv.m),
+               "s"(a.div_hkv.s), "s"(a.Hkv), "s"(a.append), "s"(a.pos0), "s"(a.Sk), "s"(a.seq_lens),
+               "s"(a.rows_total), "s"(a.div_sq.m), "s"(a.div_sq.s), "s"(a.Sq), "s"(a.ratio));
+  asm volatile("" ::"s"(a.q), "s"(a.qs_b), "s"(a.qs_h), "s"(a.qs_s), "s"(a.qs_d), "s"(a.q_vec), "s"(a.n_split),
+               "s"(a.div_ns.m), "s"(a.div_ns.s), "s"(a.kp), "s"(a.kps_b), "s"(a.kps_h), "s"(a.kps_s));
+  asm volatile("" ::"s"(a.vp), "s"(a.vps_b), "s"(a.vps_h), "s"(a.vps_s), "s"(a.ks), "s"(a.kss_b), "s"(a.kss_h),
+               "s"(a.kss_s), "s"(a.vs), "s"(a.vss_b), "s"(a.vss_h), "s"(a.vss_s));
+}
+
+// Token range [t0, t1) of split `split` over a sequence of L keys
+// (split s covers [s L / n_split, (s + 1) L / n_split)). The host keeps
+// Sk * kMaxSplit below 2^32.
 __device__ __forceinline__ void split_range(const AttnArgs& a, int L, int split, int& t0, int& t1) {
-  const uint32_t ns = (uint32_t)a.n_split;
-  t0 = (int)(((uint32_t)split * (uint32_t)L) / ns);
-  t1 = (int)(((uint32_t)(split + 1) * (uint32_t)L) / ns);
+  t0 = div_splits(a, (uint32_t)split * (uint32_t)L);
+  t1 = div_splits(a, (uint32_t)(split + 1) * (uint32_t)L);
 }
 
 // The same with split boundaries rounded down to multiples of 64 keys, so
 // that every 64-key tile of a split lies inside one page of a paged cache
 // (pages are multiples of 64 rows).
 __device__ __forceinline__ void split_range64(const AttnArgs& a, int L, int split, int& t0, int& t1) {
-  const uint32_t ns = (uint32_t)a.n_split;
-  t0 = split == 0 ? 0 : (int)((((uint32_t)split * (uint32_t)L) / ns) & ~63u);
-  t1 = split + 1 == (int)ns ? L : (int)((((uint32_t)(split + 1) * (uint32_t)L) / ns) & ~63u);
+  const int ns = a.n_split;
+  t0 = split == 0 ? 0 : (div_splits(a, (uint32_t)split * (uint32_t)L) & ~63);
+  t1 = split + 1 == ns ? L : (div_splits(a, (uint32_t)(split + 1) * (uint32_t)L) & ~63);
 }
 
 // Pool row offset of token t of a paged sequence (bt_b = its block table
@@ -247,18 +310,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+template <int NT>
 struct MergeLds {
-  float4 part_o[512];  // cross-split merge: per-thread group partials (4 dims)
-  float2 part_ml[512]; //   and their (max, sum)
-  int last;            // this workgroup merges the unit's splits
+  float4 part_o[NT];           // cross-split merge: per-thread group partials (4 dims)
+  float2 part_ml[NT];          //   and their (max, sum)
+  float2 ml[kMaxSplit * kMaxRows];  // the unit's (max, sum) pair of every (split, row)
+  int last;                    // this workgroup merges the unit's splits
 };
 
-// Partials cross between workgroups that may sit on different XCDs (each with
-// its own L2), so they are written and read with the device-scope cache
-// policy (sc1: stores write through to the device-coherent level, loads do
-// not hit a stale L2 copy). That needs no L2 writeback or invalidate, which a
-// device-scope fence would issue.
-constexpr int kSc1 = 16;  // cache-policy bits of a buffer access: SC1 (device scope)
+// Partials cross between workgroups of one unit, which all run on one XCD
+// (unit_and_split), so they travel through that XCD's L2: plain stores, and
+// loads with the sc0 policy (they miss the reading CU's L1, which may hold
+// lines of the workspace from an earlier launch, and hit the L2). Device-scope
+// stores (written through the L2) and loads measured 0.4 us slower per launch,
+// and a device-scope fence would write back and invalidate the whole L2.
+constexpr int kSc0 = 1;  // cache-policy bits of a buffer load: SC0 (miss L1)
 
 // Bits -> float through a by-value parameter. (This toolchain's
 // __builtin_bit_cast applied directly to a vector element such as v.y reads
@@ -272,19 +338,22 @@ __device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_el
 // Cross-split merge, run by the last workgroup of a unit to finish: out =
 // sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. Thread t
 // owns the 4 dims 4 (t % (D/4)) .. +4 of row (t / (D/4)) % ROWS for the
-// splits congruent to t / (ROWS*D/4) modulo P: it issues all of its partial
-// loads (16-byte output pieces and (max, sum) pairs) for a batch of 8 splits
-// at once and folds them with a running max. The P groups of threads sharing
-// a (row, 4 dims) are then combined through LDS. A row no split saw a key for
-// (all l_s = 0) yields zeros.
+// splits congruent to t / (ROWS*D/4) modulo P: it issues all of its 16-byte
+// partial loads for a batch of 8 splits at once and folds them with a running
+// max. The unit's (max, sum) pairs (one per split and row, shared by the
+// threads of a row) are read once, before the output pieces, into LDS; the
+// barrier that publishes them passes while the pieces are still in flight.
+// The P groups of threads sharing a (row, 4 dims) are then combined through
+// LDS. A row no split saw a key for (all l_s = 0) yields zeros.
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc, int kvh, int b,
-                                             MergeLds& mg) {
+                                             MergeLds<64 * NW>& mg) {
   constexpr int NT = 64 * NW;
   constexpr int Q = ROWS * D / 4;  // 16-byte pieces per split
-  static_assert(Q <= NT && NT % Q == 0 && NT <= 512, "merge mapping");
+  static_assert(Q <= NT && NT % Q == 0, "merge mapping");
   constexpr int P = NT / Q;         // thread groups per piece
   constexpr int BATCH = 8;
+  constexpr int MLPT = (kMaxSplit * ROWS + NT - 1) / NT;  // (max, sum) loads per thread
   const int tid = threadIdx.x;
   const int ns = a.n_split;
   const int piece = tid % Q, grp = tid / Q;
@@ -293,28 +362,43 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
   const __amdgpu_buffer_rsrc_t ro =
       buffer_rsrc(a.ws_o + slot0 * D, (uint32_t)((int64_t)ns * ROWS * D * 4));
   const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.ws_ml + slot0 * 2, (uint32_t)(ns * ROWS * 8));
+  const int nml = ns * ROWS;
+  uint2 mlv[MLPT];
+#pragma unroll
+  for (int k = 0; k < MLPT; ++k)  // index past nml: zeros, not stored below
+    mlv[k] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rm, (uint32_t)(tid + k * NT) * 8u, 0, kSc0));
   const int nj = (ns - grp + P - 1) / P;  // splits grp, grp + P, ... < ns
-  float Mr = kNeg, Lr = 0.0f;
-  float4 Or = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int j0 = 0; j0 < nj; j0 += BATCH) {
-    u32x4_t ov[BATCH];
-    uint2 mv[BATCH];
+  u32x4_t ov[BATCH];
+  auto issue = [&](int j0) {
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
       const uint32_t sp = (uint32_t)(grp + P * (j0 + j));  // past ns: zeros, masked below
       ov[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                              ro, (sp * Q + piece) * 16u, 0, kSc1));
-      mv[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                            rm, (sp * ROWS + r) * 8u, 0, kSc1));
+                                              ro, (sp * Q + piece) * 16u, 0, kSc0));
     }
+  };
+  issue(0);
+#pragma unroll
+  for (int k = 0; k < MLPT; ++k) {
+    const int i = tid + k * NT;
+    if (i < nml) mg.ml[i] = make_float2(u32_as_f32(mlv[k].x), u32_as_f32(mlv[k].y));
+  }
+  __syncthreads();
+  float Mr = kNeg, Lr = 0.0f;
+  float4 Or = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int j0 = 0; j0 < nj; j0 += BATCH) {
+    if (j0 > 0) issue(j0);
     // Straight-line fold (no branch per split, so every load above is in
     // flight before the first wait): splits past the last read as zero
-    // (o = 0, l = 0) and take max kNeg, so they add nothing.
-    float mj[BATCH];
+    // (o = 0) and take max kNeg and sum 0, so they add nothing.
+    float mj[BATCH], lj[BATCH];
     float mb = Mr;
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
-      mj[j] = j0 + j < nj ? u32_as_f32(mv[j].x) : kNeg;
+      const bool ok = j0 + j < nj;
+      const float2 ml = mg.ml[ok ? (grp + P * (j0 + j)) * ROWS + r : 0];
+      mj[j] = ok ? ml.x : kNeg;
+      lj[j] = ok ? ml.y : 0.0f;
       mb = fmax_nc(mb, mj[j]);
     }
     const float al = __builtin_amdgcn_exp2f(Mr - mb);
@@ -323,7 +407,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
 #pragma unroll
     for (int j = 0; j < BATCH; ++j) {
       const float f = __builtin_amdgcn_exp2f(mj[j] - mb);
-      Lr = fmaf(u32_as_f32(mv[j].y), f, Lr);
+      Lr = fmaf(lj[j], f, Lr);
       Or.x = fmaf(u32_as_f32(ov[j].x), f, Or.x);
       Or.y = fmaf(u32_as_f32(ov[j].y), f, Or.y);
       Or.z = fmaf(u32_as_f32(ov[j].z), f, Or.z);
@@ -355,10 +439,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
   const int rho = rc * ROWS + r;
   if (rho < a.rows_total) {
     const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
-    const float o4[4] = {Or.x, Or.y, Or.z, Or.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      store_from_f32(a.out, out_index(a, b, kvh, rho, 4 * d4 + k), OUT_DT, o4[k] * inv);
+    store4_from_f32(a, out_index(a, b, kvh, rho, 4 * d4), OUT_DT, Or.x * inv, Or.y * inv, Or.z * inv, Or.w * inv);
   }
 }
 
@@ -368,21 +449,20 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
 // folds the NW partials of its element (every thread reads the row's NW
 // (max, sum) pairs itself, so no serial step or extra barrier is needed) and
 // either stores the output (single split) or publishes this split's partial
-// (max, sum, o). With several splits every wave then waits until its
-// device-scope partial stores are complete, and after a barrier one thread
-// records the arrival. Arrivals are counted in two levels so that no counter
-// sees more than about eight increments per call (same-address atomics are
-// performed one after another at the memory side, and the last arrival would
-// otherwise queue behind the whole unit): split s increments sub-counter
-// s % kSubCnt of its unit; the workgroup that completes a sub-counter
-// increments the unit's top counter; the one that completes the top counter
-// arrived last, merges all partials, and re-arms the counters (each completer
-// re-arms the counter it completed) for the next call. Plans with fewer than
-// 2 * kSubCnt splits count on the top counter alone.
+// (max, sum, o). With several splits every wave then waits until its partial
+// stores are complete (acknowledged by the L2 all splits of the unit share),
+// and after a barrier one thread records the arrival with a device-scope
+// atomic add on the unit's counter. The workgroup that completes the count
+// arrived last: it merges all partials and re-arms the counter for the next
+// call. Ordering: every partial store of a split is complete before its
+// arrival is counted (s_waitcnt vmcnt(0) in each wave, then the barrier),
+// the merger's loads are issued only after its own atomic returned the final
+// count, and they miss its L1 and read the L2 the stores completed in. (One
+// counter per unit: a two-level count measured 0.3 us slower.)
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int split, int rc,
                                              int kvh, int b, const float (*o_lds)[ROWS][D],
-                                             const float (*ml_lds)[ROWS][2], MergeLds& mg) {
+                                             const float (*ml_lds)[ROWS][2], MergeLds<64 * NW>& mg) {
   constexpr int NT = 64 * NW;
   const int tid = threadIdx.x;
   const bool single = a.n_split == 1;
@@ -410,42 +490,21 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
         store_from_f32(a.out, out_index(a, b, kvh, rho, d), OUT_DT, Ls > 0.0f ? Os / Ls : 0.0f);
     } else {
       const int64_t slot = ((int64_t)unit * a.n_split + split) * ROWS + r;
-      __hip_atomic_store(a.ws_o + slot * D + d, Os, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (d == 0) {
-        __hip_atomic_store(a.ws_ml + slot * 2 + 0, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.ws_ml + slot * 2 + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      a.ws_o[slot * D + d] = Os;
+      if (d == 0) *(float2*)&a.ws_ml[slot * 2] = make_float2(M, Ls);
     }
   }
   if (single) return;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are complete
   __syncthreads();
-  if (tid == 0) {
-    const int ns = a.n_split;
-    uint32_t* cnt = a.ws_cnt + (int64_t)unit * kCntStride * (kSubCnt + 1);  // [top, sub 0..]
-    bool last;
-    if (ns >= 2 * kSubCnt) {
-      const int g = split % kSubCnt;
-      uint32_t* sub = cnt + (g + 1) * kCntStride;
-      const uint32_t n_g = (uint32_t)((ns - g + kSubCnt - 1) / kSubCnt);
-      last = false;
-      if (__hip_atomic_fetch_add(sub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == n_g - 1u) {
-        __hip_atomic_store(sub, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
-               (uint32_t)(kSubCnt - 1);
-      }
-    } else {
-      last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
-             (uint32_t)(ns - 1);
-    }
-    mg.last = last ? 1 : 0;
-  }
+  uint32_t* cnt = a.ws_cnt + (int64_t)unit * kCntStride;
+  if (tid == 0)
+    mg.last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (uint32_t)(a.n_split - 1);
   __syncthreads();
   if (!mg.last) return;
   merge_splits<ROWS, D, OUT_DT, NW>(a, unit, rc, kvh, b, mg);
-  if (tid == 0)
-    __hip_atomic_store(a.ws_cnt + (int64_t)unit * kCntStride * (kSubCnt + 1), 0u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_SYSTEM);
+  if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ===========================================================================
@@ -569,22 +628,51 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t q_lds[NW][ROWS][QROW];
   __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
   __shared__ __attribute__((aligned(16))) float ml_lds[NW][ROWS][2];
-  __shared__ MergeLds mg;
+  __shared__ MergeLds<64 * NW> mg;
   auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem);
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
+  fetch_prologue_args(a);
   int unit, split;
-  unit_and_split(a, unit, split);
-  const int rc = unit % a.row_chunks;
-  const int bh = unit / a.row_chunks;
-  const int kvh = bh % a.Hkv;
-  const int b = bh / a.Hkv;
-
+  if (!unit_and_split(a, unit, split)) return;
+  int b, kvh, rc;
+  unit_coords(a, unit, b, kvh, rc);
+  // the sequence's length is read first (its latency then overlaps the query
+  // loads, which do not depend on it)
   int L = a.append ? a.pos0 : a.Sk;
-  if (a.seq_lens) L = a.seq_lens[b];
+  if (a.seq_lens) L = load_const_i32(a.seq_lens, b);
+
+  // ---- query rows first (wave-private copy: QT pieces of 8 elements, lane
+  //      handles pieces lane, lane + 64, ...; rows past the last one read row
+  //      0 and are zeroed), then the first tiles' cache rows, so the query is
+  //      waited for without waiting for the cache ----
+  constexpr int QT = ROWS * D / 8;
+  constexpr int QPL = (QT + 63) / 64;  // query pieces per lane
+  uint4 qraw[QPL];
+#pragma unroll
+  for (int j = 0; j < QPL; ++j) {
+    const int g = lane + 64 * j;
+    const int q_r = (g / (D / 8)) % ROWS, q_k = g % (D / 8);
+    const int rho = rc * ROWS + q_r;
+    const int rho_c = rho < a.rows_total ? rho : 0;
+    const int hq = (int)fdiv((uint32_t)rho_c, a.div_sq), qi = rho_c - hq * a.Sq;
+    const int head = kvh * a.ratio + hq;
+    const int64_t qoff = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
+                         (int64_t)(8 * q_k) * a.qs_d;
+    const uint16_t* q16 = (const uint16_t*)a.q + qoff;
+    if (a.q_vec) {
+      qraw[j] = *(const uint4*)q16;
+    } else {
+      uint32_t e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[k] = q16[(int64_t)k * a.qs_d];
+      qraw[j] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+    }
+  }
+
   L = L < 0 ? 0 : L;
   // decode step: the new token goes to row L (if it fits the cache) and is
   // attended by the unit's last split from registers
@@ -667,11 +755,11 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       lim = __builtin_amdgcn_readfirstlane(ok ? min(64u, (uint32_t)t_end - t0) : 0u);
     }
   };
-  const int ng = (D + a.G - 1) / a.G;  // scales per token row: 1, 2 or 4 (wave-uniform)
+  const int ng = a.ng;  // scales per token row: 1, 2 or 4 (wave-uniform)
   const bool g32 = a.G == 32;
   uint32_t gsh[LPT];  // bit offset of each 32-dim chunk's scale in the loaded scale row
 #pragma unroll
-  for (int c = 0; c < LPT; ++c) gsh[c] = 16u * (uint32_t)((c * 32) / a.G);
+  for (int c = 0; c < LPT; ++c) gsh[c] = (a.gsh_pack >> (8 * c)) & 0xffu;
 
   // PV lane layout and the LDS slot this lane's token fills
   const int vts = lane / VLPT;
@@ -733,41 +821,17 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       }
   };
 
-  // ---- loads: the query rows first (wave-private copy: QT pieces of 8
-  //      elements, lane handles pieces lane, lane + 64, ...; rows past the last
-  //      one read row 0 and are zeroed), then the first tiles' cache rows, so
-  //      the query is waited for without waiting for the cache. Tile 0's
-  //      loads are unconditional (a wave without a tile reads past the split's
-  //      end: zeros, no memory traffic). ----
-  constexpr int QT = ROWS * D / 8;
-  constexpr int QPL = (QT + 63) / 64;  // query pieces per lane
-  uint4 qraw[QPL];
-#pragma unroll
-  for (int j = 0; j < QPL; ++j) {
-    const int g = lane + 64 * j;
-    const int q_r = (g / (D / 8)) % ROWS, q_k = g % (D / 8);
-    const int rho = rc * ROWS + q_r;
-    const int rho_c = rho < a.rows_total ? rho : 0;
-    const int head = kvh * a.ratio + rho_c / a.Sq, qi = rho_c % a.Sq;
-    const int64_t qoff = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s +
-                         (int64_t)(8 * q_k) * a.qs_d;
-    const uint16_t* q16 = (const uint16_t*)a.q + qoff;
-    if (a.q_vec) {
-      qraw[j] = *(const uint4*)q16;
-    } else {
-      uint32_t e[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) e[k] = q16[(int64_t)k * a.qs_d];
-      qraw[j] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
-    }
-  }
+  // ---- the first tiles' cache rows. Tile 0's loads are unconditional (a
+  //      wave without a tile reads past the split's end: zeros, no memory
+  //      traffic). ----
   int lim[RS][4];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int rr = rc * ROWS + rs * 4 + i;
-      int lm = a.causal ? L - a.Sq + (rr % a.Sq) + 1 : L;
+      const int qi = rr - (int)fdiv((uint32_t)rr, a.div_sq) * a.Sq;
+      int lm = a.causal ? L - a.Sq + qi + 1 : L;
       lm = lm < 0 ? 0 : lm;
       lim[rs][i] = rr < a.rows_total ? lm : 0;
     }
@@ -794,7 +858,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       page_delta(a, bt_b, tt, dl, ok);
       tt = ok ? tt + dl : Le;  // no block: the pool's end, reads zero
     }
-    const uint32_t sg = 2u * (uint32_t)((2 * (lane % (D / 2))) / a.G);
+    const uint32_t sg = 2u * fdiv(2u * (uint32_t)(lane % (D / 2)), a.div_g);
     tail_kb = __builtin_amdgcn_raw_buffer_load_b8(rk, tt * kps + col, 0, 0);
     tail_vb = __builtin_amdgcn_raw_buffer_load_b8(rv, tt * vps + col, 0, 0);
     tail_ks = __builtin_amdgcn_raw_buffer_load_b16(rks, tt * kss2 + sg, 0, 0);
@@ -1225,17 +1289,15 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   __shared__ __attribute__((aligned(16))) WT w_lds[4][CH][ROWS][LPT][TPT];
   __shared__ float o_lds[4][ROWS][D];
   __shared__ __attribute__((aligned(16))) float ml_lds[4][ROWS][2];
-  __shared__ MergeLds mg;
+  __shared__ MergeLds<256> mg;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   int unit, split;
-  unit_and_split(a, unit, split);
-  const int rc = unit % a.row_chunks;
-  const int bh = unit / a.row_chunks;
-  const int kvh = bh % a.Hkv;
-  const int b = bh / a.Hkv;
+  if (!unit_and_split(a, unit, split)) return;
+  int b, kvh, rc;
+  unit_coords(a, unit, b, kvh, rc);
 
   int L = a.Sk;
   if (a.seq_lens) {
@@ -1251,7 +1313,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   const int vts = lane / VLPT;
   const int vj = lane % VLPT;
   const int vc = vj >> 2;
-  const uint32_t gK = (uint32_t)((kc * 32) / a.G);
+  const uint32_t gK = fdiv((uint32_t)(kc * 32), a.div_g);
 
   int lim[ROWS];
   uint32_t qp[DOT2 ? ROWS : 1][16];
@@ -1262,8 +1324,9 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     const int rho = rc * ROWS + r;
     const bool row_ok = rho < a.rows_total;
     const int rho_c = row_ok ? rho : 0;
-    const int head = kvh * a.ratio + rho_c / a.Sq;
-    const int qi = rho_c % a.Sq;
+    const int hq = (int)fdiv((uint32_t)rho_c, a.div_sq);
+    const int head = kvh * a.ratio + hq;
+    const int qi = rho_c - hq * a.Sq;
     int lm = a.causal ? L - a.Sq + qi + 1 : L;
     lm = lm < 0 ? 0 : lm;
     lim[r] = row_ok ? lm : 0;
@@ -1558,13 +1621,13 @@ static int make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, 
   return KVQ_OK;
 }
 
-// Workspace: a fixed block of per-unit arrival counters (one top and kSubCnt
-// sub-counters per unit, 64 bytes apart; the same bytes for every plan, so a
-// workspace reused by calls with different plans never reads another plan's
-// partials as counters), per (unit, split, row) the partial (max, sum) pair
-// (padded to 256 bytes), then the partial output rows.
+// Workspace: a fixed block of per-unit arrival counters (64 bytes apart; the
+// same bytes for every plan, so a workspace reused by calls with different
+// plans never reads another plan's partials as counters), per (unit, split,
+// row) the partial (max, sum) pair (padded to 256 bytes), then the partial
+// output rows.
 constexpr int64_t kCntUnits = 1024;  // units a split plan may have
-static int64_t ws_cnt_bytes(const Plan&) { return kCntUnits * (kSubCnt + 1) * kCntStride * 4; }
+static int64_t ws_cnt_bytes(const Plan&) { return kCntUnits * kCntStride * 4; }
 static int64_t ws_ml_bytes(const Plan& p) {
   const int64_t slots = (int64_t)p.n_units * p.n_split * p.rows;
   return (slots * 2 * 4 + 255) / 256 * 256;
@@ -1821,10 +1884,24 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
   a.n_split = p.n_split;
   a.causal = is_causal ? 1 : 0;
   a.scale_dtype = scale_dtype;
-  a.xcd_remap = (p.n_split > 1 && p.n_units % 8 == 0) ? 1 : 0;
+  a.div_rc = make_fastdiv((uint32_t)p.row_chunks);
+  a.div_hkv = make_fastdiv((uint32_t)Hkv);
+  a.div_sq = make_fastdiv((uint32_t)Sq);
+  a.div_g = make_fastdiv((uint32_t)group_size);
+  a.div_ns = make_fastdiv((uint32_t)p.n_split);
+  a.ng = (int)((D + group_size - 1) / group_size);
+  a.gsh_pack = 0;
+  for (int c = 0; c < (int)(D / 32); ++c) a.gsh_pack |= (uint32_t)(16 * ((c * 32) / group_size)) << (8 * c);
   // 16-byte q loads need unit element stride and 16-byte aligned rows.
   a.q_vec = (q_dtype != KVQ_F32 && q_strides[3] == 1 && (uintptr_t)q % 16 == 0 &&
              q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 && q_strides[2] % 8 == 0) ? 1 : 0;
+  {
+    // 4-element output stores: unit dim stride, every row start a multiple of
+    // 4 elements, a base aligned to 4 elements (D is a multiple of 4)
+    const int64_t esz = q_dtype == KVQ_F32 ? 4 : 2;
+    a.out_vec = (out_strides[3] == 1 && out_strides[0] % 4 == 0 && out_strides[1] % 4 == 0 &&
+                 out_strides[2] % 4 == 0 && (uintptr_t)out % (4 * esz) == 0) ? 1 : 0;
+  }
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.append = step ? 1 : 0;
   a.pos0 = step ? (int)step->pos0 : 0;
@@ -1848,7 +1925,12 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
     a.ws_o = (float*)(w + ws_cnt_bytes(p) + ws_ml_bytes(p));
   }
   const bool rowmask = is_causal && Sq > 1;
-  const dim3 grid((unsigned)((int64_t)p.n_units * p.n_split));
+  // grid (8 * n_split, Y, Z), Y Z >= ceil(n_units / 8): every split of a unit
+  // on one XCD (unit_and_split)
+  const int64_t groups = (p.n_units + 7) / 8;
+  const int64_t gy = std::min<int64_t>(groups, 32768), gz = (groups + gy - 1) / gy;
+  const dim3 grid((unsigned)(8 * p.n_split), (unsigned)gy, (unsigned)gz);
+  a.grid_y = (int)gy;
   hipStream_t st = (hipStream_t)stream;
   if (D == 128) launch_d<128>(a, p, q_dtype, rowmask, grid, st);
   else launch_d<64>(a, p, q_dtype, rowmask, grid, st);

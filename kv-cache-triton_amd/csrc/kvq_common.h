@@ -114,6 +114,29 @@ __device__ __forceinline__ void page_rows(const PageMap& m, const uint32_t* b, c
   }
 }
 
+// Division by a divisor 1 <= d < 2^32 fixed at launch, for dividends
+// n < 2^32, without a divide instruction: q = (mulhi(n, m) + n) >> s with
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 < 2^32, i.e.
+// q = floor(n (2^32 + m) / 2^(32 + s)) (Granlund and Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994, section 4; the sum is
+// formed in 64 bits, so it cannot overflow). A runtime divide compiles to ~25
+// dependent scalar and vector instructions (reciprocal, conversions,
+// corrections); this is four scalar ones.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((uint64_t(1) << s) < d) ++s;
+  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)m, s};
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (uint32_t)(((uint64_t)__umulhi(n, f.m) + n) >> f.s);
+}
+
 inline int dtype_size(int dt) { return dt == KVQ_F32 ? 4 : 2; }
 inline bool dtype_ok(int dt) { return dt == KVQ_BF16 || dt == KVQ_F16 || dt == KVQ_F32; }
 

@@ -165,6 +165,17 @@ class QuantizedKVCacheBase:
                 B = int(layer.k_packed.shape[0])
                 layer.seq_lens = torch.full((B,), layer.seq_len, dtype=torch.int32, device=layer.k_packed.device)
 
+    def buffer_signature(self) -> tuple:
+        """Device addresses of every layer's buffers and device lengths. A HIP
+        graph captured over this cache holds these addresses; an edit that
+        replaces a buffer (growth, reorder, batch select, load) changes the
+        signature."""
+        return tuple(
+            (i, l.k_packed.data_ptr(), l.k_scales.data_ptr(), l.v_packed.data_ptr(), l.v_scales.data_ptr(),
+             None if l.seq_lens is None else l.seq_lens.data_ptr())
+            for i, l in sorted(self._layers.items())
+        )
+
     def room(self) -> int:
         """Tokens every layer can still take without growing its buffers."""
         return min((l.capacity - l.seq_len for l in self._layers.values()), default=0)

@@ -6,8 +6,9 @@ transformers 5.x ``GPT2Attention.forward``. Self-attention with a kvint4
 packed cache:
   * decode token, no mask, 16-bit activations -> ``append_and_attend``: one
     HIP launch quantizes the new K/V into the cache and attends over it;
-  * no mask -> ``attention_forward_quant`` (decode: fused kernel; prefill:
-    HIP dequant + SDPA), scaled by the module's ``scaling``;
+  * no mask -> ``attention_forward_quant`` over the packed cache (short query
+    blocks: fused split-K kernel; prompts: matrix-core prefill kernel), scaled
+    by the module's ``scaling``;
   * mask present -> dequantized cache through the HF attention interface.
 The reference takes the fused path at q_len == 1 even when a padding mask is
 present (:93-99), which ignores the padding; here a mask always takes the
@@ -24,6 +25,7 @@ from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 from transformers.models.gpt2.modeling_gpt2 import GPT2Attention, eager_attention_forward
 
 from .attention_quant import attention_forward_quant
+from ..module_swap import swap_attention_modules
 from ..paged_cache import PagedQuantizedKVCache
 from .kv_cache import QuantizedKVCache
 
@@ -131,19 +133,16 @@ class GPT2AttentionQuantized(GPT2Attention):
 
 
 def replace_gpt2_attention_with_quantized(model: torch.nn.Module, group_size: int = 32) -> None:
-    """In place: swap each GPT2Block self-attention for the quantized variant
-    (reference: models/gpt2/gpt2_quant.py:141-157)."""
+    """In place: swap each GPT2Block self-attention for the quantized variant,
+    reusing its Parameters (the reference copies a state dict instead,
+    models/gpt2/gpt2_quant.py:141-157). Calling it again only updates the group
+    size."""
     blocks = getattr(getattr(model, "transformer", None), "h", None)
     if blocks is None:
         raise ValueError("expected a GPT2 model with .transformer.h blocks")
-    for block in blocks:
-        old = block.attn
-        if isinstance(old, GPT2AttentionQuantized):
-            old.quant_group_size = int(group_size)
-            continue
-        param = next(old.parameters())
-        new = GPT2AttentionQuantized(old.config, layer_idx=old.layer_idx, group_size=group_size)
-        new.load_state_dict(old.state_dict())
-        new.to(device=param.device, dtype=param.dtype)
-        new.train(old.training)
-        block.attn = new
+    swap_attention_modules(
+        blocks, "attn", GPT2AttentionQuantized,
+        lambda old: GPT2AttentionQuantized(old.config, is_cross_attention=old.is_cross_attention,
+                                           layer_idx=old.layer_idx, group_size=group_size),
+        group_size,
+    )

@@ -10,9 +10,11 @@ Mirrors ``attention_forward_quant_gqa`` of ``kernels/llama3/attention_quant.py``
     returns   [B, n_q,  sq, d]               dtype of q
 
 Query head h reads KV head h // (n_q // n_kv). Decode (and short query blocks)
-run in the fused split-K kernel; long query blocks (prefill) dequantize the
-INT4 cache in HIP and run dense SDPA, so prefill also attends over the
-quantized K/V exactly as the reference's prefill does.
+run in the fused split-K kernel; prompts and long query blocks run in the
+matrix-core prefill kernel, which dequantizes each K/V tile into LDS, so a
+prefill also attends over the quantized K/V as the reference's prefill does.
+What neither kernel takes (rows beyond the fused kernel's range that the
+prefill kernel does not cover) dequantizes the cache in HIP and runs SDPA.
 
 Additions over the reference signature (keyword-only, default to the
 reference's behaviour): ``scale`` (default d**-0.5, :231) and ``seq_lens``

@@ -12,7 +12,16 @@ each, norm, LM head, argmax) is captured once into a HIP graph and replayed:
     and the captured step advances them in place;
   * position ids, the input token and the step counter are device tensors
     that the step also updates in place, so each replay feeds the next;
-  * generated tokens are written into a device [B, max_new_tokens] buffer.
+  * generated tokens are written into a device [B, max_new_tokens] buffer;
+  * the decoder owns the split-K workspace its attention launches use, so no
+    later call that grows or reuses the library's shared workspace can move it
+    under the graph, and two decoders share no arrival counters;
+  * every replay first checks that the cache still has the buffers the graph
+    was captured with (reorder, batch select, crop-and-regrow or a load
+    replace them) and raises otherwise.
+
+Batches with padding are not supported: the step runs without an attention
+mask, so every sequence of the batch must hold the same number of tokens.
 
 A replay runs the kernels of one eager step on the same buffers. The
 attention launches are the same; the library GEMMs of the projections may
@@ -29,6 +38,7 @@ import torch
 from transformers import AttentionInterface
 from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
+from .. import ops
 from ..cache_base import QuantizedKVCacheBase
 from .llama3_quant import LlamaAttentionQuantized
 
@@ -113,9 +123,16 @@ class GraphedGreedyDecoder:
         self.last_logits = torch.zeros((B, model.config.vocab_size), dtype=torch.float32, device=dev)
         self.done = 0
         self.graph = None
+        cfg = model.config
+        head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        self._workspace = torch.zeros(
+            max(1, ops.decode_workspace_bytes(B, cfg.num_attention_heads, cfg.num_key_value_heads, head_dim,
+                                              torch.bfloat16, torch.bfloat16)),
+            dtype=torch.uint8, device=dev)
         self._stream = torch.cuda.Stream(device=dev)
         self._stream.wait_stream(torch.cuda.current_stream(dev))
-        with torch.no_grad(), torch.cuda.stream(self._stream), _no_mask_creation(model):
+        with torch.no_grad(), torch.cuda.stream(self._stream), _no_mask_creation(model), \
+                ops.using_workspace(self._workspace):
             for _ in range(warmup_steps):
                 self._body()
                 self.done += 1
@@ -125,7 +142,8 @@ class GraphedGreedyDecoder:
         base = cache.host_lengths()
         fused0 = cache.fused_steps
         self.graph = torch.cuda.CUDAGraph()
-        with torch.no_grad(), _no_mask_creation(model), torch.cuda.graph(self.graph, stream=self._stream):
+        with torch.no_grad(), _no_mask_creation(model), ops.using_workspace(self._workspace), \
+                torch.cuda.graph(self.graph, stream=self._stream):
             self._body()
         cache.advance_host_lengths(base, 0)
         if cache.fused_steps - fused0 != len(base):
@@ -135,6 +153,7 @@ class GraphedGreedyDecoder:
                                f"{len(base)} cache layers; the graph would not advance every layer")
         self._base = base
         self._base_done = self.done
+        self._signature = cache.buffer_signature()
         torch.cuda.current_stream(dev).wait_stream(self._stream)
 
     def _body(self) -> None:
@@ -151,6 +170,9 @@ class GraphedGreedyDecoder:
         """Replay one decode step on the current stream."""
         if self.done >= self.max_new_tokens:
             raise RuntimeError(f"all {self.max_new_tokens} steps have run")
+        if self.cache.buffer_signature() != self._signature:
+            raise RuntimeError("the cache's buffers changed since the decode step was captured (a reorder, "
+                               "batch select, growth or load); capture a new GraphedGreedyDecoder")
         self.graph.replay()
         self.done += 1
         self.cache.advance_host_lengths(self._base, self.done - self._base_done)

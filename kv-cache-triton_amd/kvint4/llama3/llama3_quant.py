@@ -7,8 +7,10 @@ Drop-in for ``models/llama3/llama3_quant.py`` (:36-204):
         decode token, no mask -> cache.append_and_attend: one HIP launch
                     quantizes the new K/V into the cache and attends over it
         otherwise: cache.append(k, v)  (HIP quantize, written in place)
-        no mask  -> attention_forward_quant_gqa over the packed cache
-                    (decode: fused split-K kernel; prefill: HIP dequant + SDPA)
+        no mask  -> attention over the packed cache (attention_forward_quant_gqa
+                    or, for a paged cache, its attend): query blocks of up to a few
+                    rows per KV head take the fused split-K kernel, prompts and
+                    long chunks the matrix-core prefill kernel
         mask     -> dequantize the cache, HF attention interface with the mask
     else: the stock path (cache.update + HF attention interface)
     -> o_proj
@@ -34,6 +36,7 @@ from transformers.models.llama.modeling_llama import (
 )
 
 from .attention_quant import attention_forward_quant_gqa
+from ..module_swap import swap_attention_modules
 from ..paged_cache import PagedQuantizedKVCache
 from .kv_cache import QuantizedKVCache
 
@@ -141,47 +144,16 @@ class LlamaAttentionQuantized(LlamaAttention):
         return self.o_proj(attn_output), attn_weights
 
 
-def _transplant_projection(src: torch.nn.Linear, dst: torch.nn.Linear) -> None:
-    """Rebind weight/bias Parameters from ``src`` to ``dst`` and move any
-    ``accelerate`` hook (reference: models/llama3/llama3_quant.py:146-168)."""
-    dst.weight = src.weight
-    dst.bias = src.bias if getattr(src, "bias", None) is not None else None
-    hook = getattr(src, "_hf_hook", None)
-    if hook is not None:
-        try:
-            from accelerate.hooks import add_hook_to_module, remove_hook_from_module
-
-            remove_hook_from_module(src)
-            add_hook_to_module(dst, hook)
-        except Exception:
-            pass
-
-
 def replace_llama_attention_with_quantized(model: torch.nn.Module, group_size: int = 32) -> None:
     """In place: swap each Llama decoder layer's self-attention for the
-    quantized variant, reusing the projection Parameters (no copies). Calling
-    it again only updates the group size (reference :171-204)."""
+    quantized variant, reusing the projection Parameters (no copies) and moving
+    any accelerate hooks. Calling it again only updates the group size
+    (reference: models/llama3/llama3_quant.py:171-204)."""
     layers = getattr(getattr(model, "model", None), "layers", None)
     if layers is None:
         raise ValueError("expected a Llama CausalLM model with .model.layers")
-    try:
-        from accelerate.hooks import add_hook_to_module, remove_hook_from_module
-
-        have_accel = True
-    except Exception:
-        have_accel = False
-
-    for layer in layers:
-        old = layer.self_attn
-        if isinstance(old, LlamaAttentionQuantized):
-            old.quant_group_size = int(group_size)
-            continue
-        new = LlamaAttentionQuantized(old.config, layer_idx=old.layer_idx, group_size=group_size)
-        for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
-            _transplant_projection(getattr(old, name), getattr(new, name))
-        old_hook = getattr(old, "_hf_hook", None)
-        if have_accel and old_hook is not None:
-            remove_hook_from_module(old)
-            add_hook_to_module(new, old_hook)
-        new.train(old.training)
-        layer.self_attn = new
+    swap_attention_modules(
+        layers, "self_attn", LlamaAttentionQuantized,
+        lambda old: LlamaAttentionQuantized(old.config, layer_idx=old.layer_idx, group_size=group_size),
+        group_size,
+    )

@@ -12,6 +12,7 @@ Layouts (bit-identical to the reference's, ``kernels/llama3/quantize.py:7-14``):
 
 from __future__ import annotations
 
+import contextlib
 import math
 import threading
 
@@ -207,30 +208,80 @@ class _Workspaces:
     """Zero-initialised split-K workspaces, one per (device, stream).
 
     The kernel returns its counters to zero, so a workspace is reused across
-    calls issued on the same stream (which are ordered).
+    calls issued on the same stream (which are ordered). A HIP graph captured
+    on a stream keeps the address of the workspace it was captured with, so a
+    buffer is never freed once handed out: when a later call needs more bytes
+    the key gets a new, larger buffer and the old one stays allocated (the
+    retired buffers together are at most the size of the current one, since
+    sizes at least double). Inside ``using_workspace(buf)`` calls on this
+    thread take ``buf`` instead (a graph that owns its workspace: two graphs
+    replayed concurrently then share no counters).
     """
 
     def __init__(self) -> None:
         self._lock = threading.Lock()
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
+        self._local = threading.local()
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        own = getattr(self._local, "buf", None)
+        if own is not None:
+            if own.device != device or own.numel() < nbytes:
+                raise ValueError(f"the workspace given to using_workspace ({own.numel()} bytes on {own.device}) "
+                                 f"is too small or on another device: {nbytes} bytes needed on {device}")
+            return own
+        idx = device.index
+        if idx is None:
+            idx = torch.cuda.current_device() if device.type == "cuda" else -1
+        key = (idx, stream)
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
                 size = max(nbytes, 1 << 20)
                 if buf is not None:
                     size = max(size, 2 * buf.numel())
+                    self._retired.append(buf)
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
+
+    @contextlib.contextmanager
+    def using(self, buf: torch.Tensor):
+        if buf.dtype != torch.uint8 or buf.dim() != 1:
+            raise ValueError("a workspace is a 1-D uint8 tensor")
+        prev = getattr(self._local, "buf", None)
+        self._local.buf = buf
+        try:
+            yield buf
+        finally:
+            self._local.buf = prev
 
 
 _workspaces = _Workspaces()
 # prefill split partials: a separate buffer, so that they never overwrite the
 # decode kernels' arrival counters
 _prefill_workspaces = _Workspaces()
+
+
+def decode_workspace_bytes(B: int, Hq: int, Hkv: int, D: int, q_dtype: torch.dtype,
+                           scale_dtype: torch.dtype, Sq: int = 1, n_split: int = 64) -> int:
+    """Workspace bytes that cover every decode launch of this shape with up to
+    `n_split` splits (64 is the library's largest split count)."""
+    lib = nat.lib()
+    n = lib.kvq_decode_attn_workspace_bytes(B, Hq, Hkv, Sq, D, nat.DTYPE_CODE[q_dtype],
+                                            nat.DTYPE_CODE[scale_dtype], n_split)
+    if n < 0:
+        nat.check(int(n), "kvq_decode_attn_workspace_bytes")
+    return int(n)
+
+
+def using_workspace(buf: torch.Tensor):
+    """Context manager: decode launches made on this thread inside it use the
+    zero-filled uint8 device tensor `buf` as their split-K workspace (size it
+    with decode_workspace_bytes). Launches that overlap in time must not share
+    one workspace."""
+    return _workspaces.using(buf)
 
 
 def _prefill_ws(q: torch.Tensor, Hkv: int, Sk: int, stream: int) -> tuple:

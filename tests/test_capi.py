@@ -65,11 +65,11 @@ def test_workspace_bytes():
     # a requested split count is kept whatever the kernel's minimum split
     # length (the VALU kernel's is 1024 keys): 12 units x 3 splits of partials
     ws3 = lib.kvq_decode_attn_workspace_bytes(1, 12, 12, 1, 64, nat.KVQ_F32, nat.KVQ_F16, 3)
-    assert ws3 == 1024 * 5 * 64 + 512 + 12 * 3 * 64 * 4  # counters, (max, sum) pairs padded to 256 B, partials
+    assert ws3 == 1024 * 64 + 512 + 12 * 3 * 64 * 4  # counters, (max, sum) pairs padded to 256 B, partials
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 1) == 0
     ws = lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, B16, B16, 32)
-    # counter block (1024 units x 5 counters x 64 bytes), then 8 units x 32 splits x 4 rows x (128 + 2) floats
-    assert ws == 1024 * 5 * 64 + 8 * 32 * 4 * 130 * 4
+    # counter block (1024 units x one counter x 64 bytes), then 8 units x 32 splits x 4 rows x (128 + 2) floats
+    assert ws == 1024 * 64 + 8 * 32 * 4 * 130 * 4
     assert lib.kvq_decode_attn_workspace_bytes(1, 32, 8, 1, 128, 7, B16, 4) == nat.KVQ_EINVAL
 
 

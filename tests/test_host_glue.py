@@ -209,3 +209,28 @@ def test_graph_decoder_rejects_unswapped_models_and_other_caches():
         GraphedGreedyDecoder(model, QuantizedKVCache(), tok, max_new_tokens=4)
     with pytest.raises(TypeError):
         GraphedGreedyDecoder(model, PagedQuantizedKVCache(), tok, max_new_tokens=4)
+
+
+def test_workspace_growth_keeps_captured_buffers_alive():
+    """A HIP graph keeps the address of the split-K workspace it was captured
+    with. When a later call on the same (device, stream) needs a larger one,
+    the old buffer must stay allocated (retired, not freed), and a private
+    workspace given with using_workspace takes precedence on this thread."""
+    ws = ops._Workspaces()
+    dev = torch.device("cpu")
+    small = ws.get(dev, 7, 1000)
+    ptr = small.data_ptr()
+    assert ws.get(dev, 7, 500) is small  # large enough: reused
+    big = ws.get(dev, 7, 3 << 20)
+    assert big is not small and big.numel() >= 3 << 20
+    assert any(t.data_ptr() == ptr for t in ws._retired), "the replaced buffer was dropped"
+    assert ws.get(dev, 8, 10) is not big  # another stream, another buffer
+    own = torch.zeros(4096, dtype=torch.uint8)
+    with ws.using(own):
+        assert ws.get(dev, 7, 4096) is own
+        with pytest.raises(ValueError):
+            ws.get(dev, 7, 8192)
+    assert ws.get(dev, 7, 10) is big
+    with pytest.raises(ValueError):
+        with ws.using(torch.zeros(4, dtype=torch.float32)):
+            pass
