@@ -18,20 +18,25 @@ half-precision batched GEMM on the GPU):
 Q is teacher-forced with F's greedy tokens, so both see the same inputs at
 every step. Bars, the reference's (tests/llama3/test_llama3_quant_decode.py:
 61-80), on Q against F: prefill last-logit max-abs < 1.0 with the same
-argmax, every decode step < 2.0, and the same greedy token at >= 16 of the
-64 steps (the reference's generate test asks a prefix of 4 of 16,
-tests/llama3/test_llama3_generate_parity.py:52-74). The prefill argmax is
+argmax, every decode step < 2.0, and the same greedy token at >= 48 of the
+64 steps (56 measured; the reference's generate test asks a prefix of 4 of
+16, tests/llama3/test_llama3_generate_parity.py:52-74). The prefill argmax is
 compared exactly when F's top-2 logit margin exceeds twice the measured
 max-abs difference. Below that, a different attention kernel can swap a
 near-tie, and Q's token must then be F's runner-up. On this prompt F's margin
 is 0.031, against 0.33 between Q's matrix-core prefill and F's flash SDPA.
 
-Q against R (INT4 against bf16 KV) is printed, not asserted: this random-init
-network amplifies the INT4 rounding of K/V, by itself, to a relative change
-of about 0.4 in the hidden state after 4 layers and 0.8 at the last, and
-max-abs 5 on logits of std 1.3 (the same figures for F against R, so the
-format and not the implementation sets them; rounding K/V to fp16 instead
-moves the logits by 0.07).
+Q against R (INT4 against the bf16 DynamicCache, the north star's check) has
+its own stated tolerance: this random-init network amplifies the INT4
+rounding of K/V, by itself, to a relative change of about 0.4 in the hidden
+state after 4 layers and 0.8 at the last, and max-abs ~5 on logits of std 1.3,
+so the reference's absolute bars (set on pretrained models) cannot hold
+against R for any INT4 implementation here, including the reference's own
+semantics F. The bound is therefore relative to what the format itself
+costs, measured in the same run: at the prefill and at every decode step,
+max-abs(Q - R) <= max-abs(F - R) + 0.5, and Q's greedy tokens agree with R's
+at no fewer steps than F's do, minus 4 of 64. (Rounding K/V to fp16 instead
+of INT4 moves the logits by 0.07, so the gap is the 4-bit format's.)
 The test also prints ms per decode token of Q (HF eager, Python overhead
 included) and the KV bytes of both caches.
 """
@@ -130,12 +135,19 @@ def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
         agree = int((own_f == own_q).sum().item())
         d0_r = (first_r - first_q).abs().max().item()
         diffs_r = _diffs(logits_r, logits_q)
-        agree_r = int((torch.stack([l.argmax(-1) for l in logits_r], 1) == own_q).sum().item())
+        own_r = torch.stack([l.argmax(-1) for l in logits_r], 1)
+        agree_r = int((own_r == own_q).sum().item())
+        d0_fr = (first_r - first_f).abs().max().item()
+        diffs_fr = _diffs(logits_r, logits_f)
+        agree_fr = int((own_r == own_f).sum().item())
         print(f"C3 INT4 (Q) vs INT4 dense reference (F): prefill last-logit max-abs {d0:.4f}; decode max-abs "
               f"max {max(diffs):.4f} mean {statistics.fmean(diffs):.4f}; same greedy token {agree}/{STEPS}")
         print(f"C3 INT4 (Q) vs bf16 DynamicCache (R): prefill max-abs {d0_r:.4f}; decode max-abs max "
               f"{max(diffs_r):.4f} mean {statistics.fmean(diffs_r):.4f}; same greedy token {agree_r}/{STEPS}; "
               f"logits std {first_r.std().item():.3f}")
+        print(f"C3 INT4 dense reference (F) vs bf16 DynamicCache (R): prefill max-abs {d0_fr:.4f}; decode "
+              f"max-abs max {max(diffs_fr):.4f} mean {statistics.fmean(diffs_fr):.4f}; same greedy token "
+              f"{agree_fr}/{STEPS}")
         print(f"C3 INT4 decode ms/token median {1e3 * statistics.median(secs_q):.2f} (HF eager); KV bytes: "
               f"DynamicCache {ref_kv_bytes / 2**20:.0f} MiB, INT4 {q_cache.nbytes() / 2**20:.0f} MiB")
         top2 = first_f[0].topk(2)
@@ -151,7 +163,12 @@ def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
             assert first_q.argmax().item() in top2.indices.tolist()
         for step, d in enumerate(diffs):
             assert d < 2.0, f"decode step {step}: {d}"
-        assert agree >= STEPS // 4
+        assert agree >= 48, f"Q and F pick the same greedy token at {agree} of {STEPS} steps"
+        # against the bf16 DynamicCache: within what the INT4 format itself costs (F vs R) + 0.5
+        assert d0_r <= d0_fr + 0.5, f"prefill: |Q - R| {d0_r:.3f} > |F - R| {d0_fr:.3f} + 0.5"
+        for step, (dq, df) in enumerate(zip(diffs_r, diffs_fr)):
+            assert dq <= df + 0.5, f"decode step {step}: |Q - R| {dq:.3f} > |F - R| {df:.3f} + 0.5"
+        assert agree_r >= agree_fr - 4, f"greedy agreement with R: Q {agree_r}, F {agree_fr}" 
     finally:
         del model
         torch.cuda.empty_cache()
