@@ -90,6 +90,11 @@ def main() -> int:
     ap.add_argument("--model", action="store_true",
                     help="whole-model decode instead: random-init Llama-3.1-8B (C3), 16K prompt, 64 greedy "
                          "steps over the INT4 cache, each step one HIP graph replay")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="the ceiling instead: a streaming-read kernel over the decode step's bytes (one buffer "
+                         "per layer, several grids), its per-wave clock stamps, and the decode step's phases "
+                         "from the instrumented build of the kernel; one JSON line")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the streaming-read ceiling in the bench line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="wall budget of the CPU sample (the torch path; the C restatement gets a quarter)")
@@ -133,59 +138,20 @@ def main() -> int:
         return prefill_bench(args, w)
     if args.model:
         return model_bench(args)
+    if args.stream_probe:
+        return stream_probe_bench(args, w)
     B, Hq, Hkv, D, G, ctx, L = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"], w["layers"]
-    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w["dtype"]]
-    sdt = torch.float16 if w["dtype"] != "bf16" else torch.bfloat16  # GPT-2: fp16 scales
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(dev)
-    gen = torch.Generator(device=dev).manual_seed(1)
     S_cap = ctx + 1
     W_ = ops.packed_width(D, G)
     NG = ops.num_groups(D, G)
-
-    # ---- synthetic per-layer caches, filled by the HIP quantizer ----
-    seq_lens = None
-    if w["ragged"]:
-        lens = torch.randint(128, ctx + 1, (B,), generator=torch.Generator().manual_seed(4))
-        seq_lens = lens.to(dev, torch.int32)
     P = args.paged
-    pt = None
-    if P:
-        if P < 64 or P & (P - 1):
-            print("bench.py: --paged needs a power of two >= 64", file=sys.stderr)
-            return 2
-        pages = -(-S_cap // P)
-        n_blocks = B * pages
-        perm = torch.randperm(n_blocks, generator=torch.Generator().manual_seed(5)).to(torch.int32)
-        pt = ops.PageTable(perm.view(B, pages).contiguous().to(dev), P, n_blocks)
-    layers = []
-    with torch.cuda.stream(stream):
-        for _ in range(L):
-            if P:
-                kp = torch.empty(Hkv, pt.num_blocks * P, W_, dtype=torch.uint8, device=dev)
-                ks = torch.empty(Hkv, pt.num_blocks * P, NG, dtype=sdt, device=dev)
-            else:
-                kp = torch.empty(B, Hkv, S_cap, W_, dtype=torch.uint8, device=dev)
-                ks = torch.empty(B, Hkv, S_cap, NG, dtype=sdt, device=dev)
-            vp = torch.empty_like(kp)
-            vs = torch.empty_like(ks)
-            for packed, scales in ((kp, ks), (vp, vs)):
-                x = torch.randn(B, Hkv, ctx, D, generator=gen, device=dev, dtype=torch.float32).to(tdt)
-                if P:
-                    ops.quantize_into_paged(x, packed, scales, pt, G, 0)
-                else:
-                    ops.quantize_into(x, packed, scales, G, 0)
-                del x
-            layer = dict(
-                kp=kp, ks=ks, vp=vp, vs=vs,
-                knew=torch.randn(B, Hkv, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
-                vnew=torch.randn(B, Hkv, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
-                q=torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
-                out=torch.empty(B, Hq, 1, D, device=dev, dtype=tdt),
-            )
-            layers.append(layer)
-    torch.cuda.synchronize()
+    if P and (P < 64 or P & (P - 1)):
+        print("bench.py: --paged needs a power of two >= 64", file=sys.stderr)
+        return 2
+    layers, seq_lens, pt = make_layers(w, P, dev, stream)
 
     pos = seq_lens if seq_lens is not None else ctx
     attended = ctx + 1
@@ -358,8 +324,294 @@ def main() -> int:
         },
     }
 
+    if not args.no_ceiling and P == 0:
+        # the same bytes read by a kernel that does nothing else (one buffer
+        # per layer, the best of a few grids): how much of the HBM peak a
+        # launch of this size can reach at all
+        ceil = stream_ceiling(k_bytes, L, dev, stream, CEILING_GRIDS)
+        best = min(ceil, key=lambda r: r["us_per_launch"])
+        result["roofline"]["ceiling"] = {
+            "achieved": best["gbs"], "unit": "GB/s", "frac_of_peak": round(best["gbs"] / HBM_PEAK_GBS, 4),
+            "decode_frac_of_ceiling": round(achieved / best["gbs"], 4), "grid": best["grid"],
+            "block": best["block"], "kernel": "stream_read (libkvq_probe.so)",
+        }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, layers, attended, seq_lens, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def make_layers(w: dict, P: int, dev, stream):
+    """The workload's synthetic per-layer caches, filled by the HIP quantizer
+    from seeded torch.randn, plus each layer's new K/V rows, query and output.
+    Returns (layers, seq_lens or None, page table or None)."""
+    import torch
+
+    from kvint4 import ops
+
+    B, Hq, Hkv, D, G, ctx, L = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"], w["layers"]
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w["dtype"]]
+    sdt = torch.float16 if w["dtype"] != "bf16" else torch.bfloat16  # GPT-2: fp16 scales
+    gen = torch.Generator(device=dev).manual_seed(1)
+    S_cap = ctx + 1
+    W_ = ops.packed_width(D, G)
+    NG = ops.num_groups(D, G)
+    seq_lens = None
+    if w["ragged"]:
+        lens = torch.randint(128, ctx + 1, (B,), generator=torch.Generator().manual_seed(4))
+        seq_lens = lens.to(dev, torch.int32)
+    pt = None
+    if P:
+        pages = -(-S_cap // P)
+        n_blocks = B * pages
+        perm = torch.randperm(n_blocks, generator=torch.Generator().manual_seed(5)).to(torch.int32)
+        pt = ops.PageTable(perm.view(B, pages).contiguous().to(dev), P, n_blocks)
+    layers = []
+    with torch.cuda.stream(stream):
+        for _ in range(L):
+            if P:
+                kp = torch.empty(Hkv, pt.num_blocks * P, W_, dtype=torch.uint8, device=dev)
+                ks = torch.empty(Hkv, pt.num_blocks * P, NG, dtype=sdt, device=dev)
+            else:
+                kp = torch.empty(B, Hkv, S_cap, W_, dtype=torch.uint8, device=dev)
+                ks = torch.empty(B, Hkv, S_cap, NG, dtype=sdt, device=dev)
+            vp = torch.empty_like(kp)
+            vs = torch.empty_like(ks)
+            for packed, scales in ((kp, ks), (vp, vs)):
+                x = torch.randn(B, Hkv, ctx, D, generator=gen, device=dev, dtype=torch.float32).to(tdt)
+                if P:
+                    ops.quantize_into_paged(x, packed, scales, pt, G, 0)
+                else:
+                    ops.quantize_into(x, packed, scales, G, 0)
+                del x
+            layer = dict(
+                kp=kp, ks=ks, vp=vp, vs=vs,
+                knew=torch.randn(B, Hkv, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
+                vnew=torch.randn(B, Hkv, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
+                q=torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.float32).to(tdt),
+                out=torch.empty(B, Hq, 1, D, device=dev, dtype=tdt),
+            )
+            layers.append(layer)
+    torch.cuda.synchronize()
+    return layers, seq_lens, pt
+
+
+# (grid, block) of the streaming-read probe: whole-GPU fills from one
+# workgroup per CU to eight
+PROBE_GRIDS = ((256, 256), (256, 512), (256, 1024), (512, 256), (512, 512), (1024, 256), (1024, 512),
+               (2048, 256), (2048, 512))
+CEILING_GRIDS = ((256, 512), (512, 256), (1024, 256), (2048, 256))
+
+
+def probe_lib():
+    """libkvq_probe.so: the streaming-read probe and the phase-stamped build of
+    the decode kernels (measurement only; never used by the product path)."""
+    import ctypes
+
+    from kvint4 import _native as nat
+
+    path = os.path.join(ROOT, "kv-cache-triton_amd", "kvint4", "libkvq_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(path)
+    prod = nat.lib()
+    for name in ("kvq_decode_step", "kvq_decode_attn_num_splits", "kvq_decode_attn_workspace_bytes", "kvq_last_error"):
+        fn = getattr(lib, name)
+        fn.restype = getattr(prod, name).restype
+        fn.argtypes = getattr(prod, name).argtypes
+    lib.kvq_probe_stream_read.restype = ctypes.c_int
+    lib.kvq_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.kvq_probe_set_phase_stamps.restype = ctypes.c_int
+    lib.kvq_probe_set_phase_stamps.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
+    """Streaming read of nbytes (rounded up to 16) from each of L buffers, one
+    launch per buffer captured in a HIP graph and replayed 20 times between
+    two events on the launch stream: per (grid, block), the average launch
+    time and GB/s over nbytes."""
+    import torch
+
+    lib = probe_lib()
+    n = -(-nbytes // 16) * 16
+    g = torch.Generator(device=dev).manual_seed(7)
+    bufs = [torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev, generator=g) for _ in range(L)]
+    sink = torch.zeros(max(gr for gr, _ in grids), dtype=torch.int32, device=dev)
+    out = []
+    for grid, block in grids:
+        graph = torch.cuda.CUDAGraph()
+        per = 0
+        with torch.cuda.graph(graph, stream=stream):
+            for b in bufs:
+                per = lib.kvq_probe_stream_read(b.data_ptr(), n, grid, block, sink.data_ptr(), None,
+                                                stream.cuda_stream)
+        if per <= 0:
+            continue
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                graph.replay()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(20):
+                graph.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (20 * L)
+        out.append({"grid": grid, "block": block, "pieces_per_thread": per, "us_per_launch": round(us, 3),
+                    "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    if keep is not None:
+        keep.extend(bufs)
+    return out
+
+
+def _dist(vals) -> dict:
+    import numpy as np
+
+    v = np.sort(np.asarray(vals, dtype=np.float64))
+    if v.size == 0:
+        return {}
+    q = lambda f: round(float(v[min(v.size - 1, int(f * v.size))]), 0)
+    return {"n": int(v.size), "min": q(0.0), "p10": q(0.1), "med": q(0.5), "p90": q(0.9), "max": round(float(v[-1]), 0)}
+
+
+def stream_probe_bench(args, w: dict) -> int:
+    """--stream-probe: what a launch of the decode step's size can reach, and
+    where the decode step's time goes. Prints one JSON line:
+    - stream: the streaming-read kernel over the step's bytes, per grid;
+    - stream_phases_ns: its per-wave clock stamps on a cold buffer (entry, all
+      loads issued, first and last data arrived), ns after the first wave;
+    - decode_step: the product kernel's launch time (graph of the workload's
+      layers, as the bench line) and its fraction of the best read;
+    - decode_phases_ns: the instrumented build of the same kernel on a cold
+      layer, per point (entry, loads issued, keys / values of the first tile
+      arrived, tile loop done, workgroup fold done, partial acknowledged,
+      arrival counted, merge start, merge inputs arrived, merged, exit)."""
+    import numpy as np
+    import torch
+
+    from kvint4 import _native as nat
+    from kvint4 import ops
+
+    if w["dtype"] == "f32" or w["ragged"]:
+        print("bench.py: --stream-probe takes a 16-bit workload with one length for the batch", file=sys.stderr)
+        return 2
+    B, Hq, Hkv, D, G, ctx, L = w["B"], w["Hq"], w["Hkv"], w["D"], w["G"], w["ctx"], w["layers"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    lib = probe_lib()
+    nbytes = attn_bytes(w, B * ctx) + append_bytes(w)  # what one decode-step launch must move
+    keep = []
+    stream_rows = stream_ceiling(nbytes, L, dev, stream, PROBE_GRIDS, keep)
+    best = min(stream_rows, key=lambda r: r["us_per_launch"])
+
+    # per-wave stamps of the read on a cold buffer (the other buffers read first)
+    n = -(-nbytes // 16) * 16
+    grid, block = 256, 512
+    waves = grid * (block // 64)
+    st = torch.zeros(grid * 16 * 4, dtype=torch.int64, device=dev)
+    sink = torch.zeros(grid, dtype=torch.int32, device=dev)
+    with torch.cuda.stream(stream):
+        for b in keep[1:]:
+            lib.kvq_probe_stream_read(b.data_ptr(), n, grid, block, sink.data_ptr(), None, stream.cuda_stream)
+        rc = lib.kvq_probe_stream_read(keep[0].data_ptr(), n, grid, block, sink.data_ptr(), st.data_ptr(),
+                                       stream.cuda_stream)
+    torch.cuda.synchronize()
+    if rc <= 0:
+        print("bench.py: stamped streaming read did not launch", file=sys.stderr)
+        return 1
+    s = st.view(grid, 16, 4)[:, : block // 64].reshape(waves, 4).cpu().numpy()
+    t0 = s[:, 0].min()
+    names = ("entry", "loads_issued", "first_arrived", "all_arrived")
+    stream_phases = {nm: _dist((s[:, k] - t0) * 10.0) for k, nm in enumerate(names)}
+    del keep
+
+    # the decode step: product kernel timing, then the instrumented build's phases
+    layers, _, _ = make_layers(w, 0, dev, stream)
+    sm_scale = D ** -0.5
+
+    def step():
+        for layer in layers:
+            ops.decode_step(layer["q"], layer["knew"], layer["vnew"], layer["kp"], layer["ks"], layer["vp"],
+                            layer["vs"], ctx, n_kv_heads=Hkv, group_size=G, sm_scale=sm_scale, out=layer["out"])
+
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        graph.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(20):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    dec_us = e0.elapsed_time(e1) * 1e3 / (20 * L)
+    dec_bytes = attn_bytes(w, B * ctx) + append_bytes(w)
+
+    qd, sd = nat.DTYPE_CODE[layers[0]["q"].dtype], nat.DTYPE_CODE[layers[0]["ks"].dtype]
+    cap = int(layers[0]["kp"].shape[2])
+    ns = lib.kvq_decode_attn_num_splits(B, Hq, Hkv, 1, D, ctx + 1, qd, sd, ops._num_cus(dev))
+    ws_bytes = lib.kvq_decode_attn_workspace_bytes(B, Hq, Hkv, 1, D, qd, sd, ns)
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    n_wg = 8 * ns * -(-(B * Hkv * -(-(Hq // Hkv) // 8)) // 8)  # launched workgroups (one row chunk per unit)
+    ph = torch.zeros(n_wg * 16 * 16, dtype=torch.int64, device=dev)
+
+    def stamped(layer) -> None:
+        rc = lib.kvq_decode_step(
+            layer["q"].data_ptr(), qd, nat.i64_array(layer["q"].stride()),
+            layer["knew"].data_ptr(), nat.i64_array(layer["knew"].stride()),
+            layer["vnew"].data_ptr(), nat.i64_array(layer["vnew"].stride()),
+            layer["kp"].data_ptr(), nat.i64_array(layer["kp"].stride()[:3]),
+            layer["ks"].data_ptr(), nat.i64_array(layer["ks"].stride()[:3]),
+            layer["vp"].data_ptr(), nat.i64_array(layer["vp"].stride()[:3]),
+            layer["vs"].data_ptr(), nat.i64_array(layer["vs"].stride()[:3]),
+            sd, layer["out"].data_ptr(), nat.i64_array(layer["out"].stride()),
+            B, Hq, Hkv, D, G, cap, None, ctx, float(sm_scale), ns, ws.data_ptr(), ws.numel(),
+            stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"instrumented kvq_decode_step: {lib.kvq_last_error().decode()}")
+
+    with torch.cuda.stream(stream):
+        for layer in layers[1:]:
+            stamped(layer)  # stamps off (null buffer): evicts layer 0's cache from the caches
+    torch.cuda.synchronize()
+    if lib.kvq_probe_set_phase_stamps(ph.data_ptr()) != 0:
+        raise RuntimeError("kvq_probe_set_phase_stamps failed")
+    with torch.cuda.stream(stream):
+        stamped(layers[0])
+    torch.cuda.synchronize()
+    lib.kvq_probe_set_phase_stamps(None)
+    a = ph.view(n_wg, 16, 16).cpu().numpy()
+    nz = a[:, :, 0] > 0
+    t0 = a[:, :, 0][nz].min()
+    points = ("entry", "loads_issued", "keys_arrived", "values_arrived", "tile_loop_done", "wg_fold_done",
+              "partial_acked", "arrival_counted", "merge_start", "merge_inputs_arrived", "merged", "exit")
+    dec_phases = {}
+    for k, nm in enumerate(points):
+        v = a[:, :, k]
+        v = v[v > 0]
+        if v.size:
+            dec_phases[nm] = _dist((v - t0) * 10.0)
+    result = {
+        "metric": "streaming-read ceiling and decode-step phases (one MI355X)",
+        "workload": w["desc"], "bytes_per_launch": nbytes, "layers": L,
+        "stream": stream_rows, "best": best,
+        "stream_phases_ns": dict(stream_phases, grid=grid, block=block),
+        "decode_step": {"us_per_launch": round(dec_us, 3), "gbs": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
+                        "frac_of_peak": round(dec_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "frac_of_best_read": round(best["us_per_launch"] / dec_us, 4), "n_split": int(ns)},
+        "decode_phases_ns": dec_phases,
+    }
     print(json.dumps(result), flush=True)
     return 0
 

@@ -52,6 +52,34 @@
 
 namespace kvq {
 
+// Phase stamps (instrumented builds only: -DKVQ_PHASE_STAMPS, the measurement
+// library behind bench.py --stream-probe; the product library compiles these
+// to nothing). Lane 0 of each wave writes the 100 MHz s_memrealtime clock at
+// fixed points of the decode step into a.stamps[(workgroup * 16 + wave) *
+// kPhaseSlots + point] (a kernel argument, so the pointer sits in scalar
+// registers and a stamp is one clock read and one store); KVQ_STAMP_AFTER
+// first waits for the value x (a load result), so the stamp marks its arrival.
+constexpr int kPhaseSlots = 16;
+#if defined(KVQ_PHASE_STAMPS)
+#define KVQ_STAMP(point) ::kvq::phase_stamp(a.stamps, point)
+#define KVQ_STAMP_AFTER(point, x)          \
+  do {                                     \
+    asm volatile("" ::"v"(x));             \
+    ::kvq::phase_stamp(a.stamps, point);   \
+  } while (0)
+#else
+#define KVQ_STAMP(point) \
+  do {                   \
+  } while (0)
+#define KVQ_STAMP_AFTER(point, x) \
+  do {                            \
+  } while (0)
+#endif
+// Stamp points: 0 entry, 1 first tiles' loads issued, 2 first tile's keys
+// arrived, 3 its values arrived, 4 tile loop done, 5 workgroup fold done,
+// 6 partial stores acknowledged, 7 arrival counted (thread 0), 8 merge start,
+// 9 merge inputs arrived, 10 merged output computed, 11 exit.
+
 struct AttnArgs {
   const void* q;
   int64_t qs_b, qs_h, qs_s, qs_d;
@@ -97,7 +125,23 @@ struct AttnArgs {
                      // (zero between calls)
   float* ws_ml;      // [n_units][n_split][ROWS][2]  (max, sum)
   float* ws_o;       // [n_units][n_split][ROWS][D]
+#if defined(KVQ_PHASE_STAMPS)
+  unsigned long long* stamps;  // phase stamps, or null
+#endif
 };
+
+#if defined(KVQ_PHASE_STAMPS)
+__device__ __forceinline__ void phase_stamp(unsigned long long* p, int point) {
+  // compiler fences: no memory operation moves across the clock read
+  asm volatile("" ::: "memory");
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  asm volatile("" ::: "memory");
+  if (p != nullptr && (threadIdx.x & 63) == 0) {
+    const size_t wg = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z);
+    p[(wg * 16 + (threadIdx.x >> 6)) * kPhaseSlots + point] = t;
+  }
+}
+#endif
 
 constexpr float kNeg = -1.0e30f;
 constexpr int kMaxSplit = 64;  // split-K fan-out cap (bounds the merge's LDS)
@@ -388,6 +432,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
   float4 Or = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int j0 = 0; j0 < nj; j0 += BATCH) {
     if (j0 > 0) issue(j0);
+    if (j0 == 0) KVQ_STAMP_AFTER(9, ov[BATCH - 1].x);
     // Straight-line fold (no branch per split, so every load above is in
     // flight before the first wait): splits past the last read as zero
     // (o = 0) and take max kNeg and sum 0, so they add nothing.
@@ -436,6 +481,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
       Or.z = fmaf(o.z, f, Or.z); Or.w = fmaf(o.w, f, Or.w);
     }
   }
+  KVQ_STAMP_AFTER(10, Lr);
   const int rho = rc * ROWS + r;
   if (rho < a.rows_total) {
     const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
@@ -495,14 +541,18 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
     }
   }
   if (single) return;
+  KVQ_STAMP(5);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are complete
+  KVQ_STAMP(6);
   __syncthreads();
   uint32_t* cnt = a.ws_cnt + (int64_t)unit * kCntStride;
   if (tid == 0)
     mg.last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               (uint32_t)(a.n_split - 1);
+    KVQ_STAMP(7);
   __syncthreads();
   if (!mg.last) return;
+  KVQ_STAMP(8);
   merge_splits<ROWS, D, OUT_DT, NW>(a, unit, rc, kvh, b, mg);
   if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -635,6 +685,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
+  KVQ_STAMP(0);
   fetch_prologue_args(a);
   int unit, split;
   if (!unit_and_split(a, unit, split)) return;
@@ -845,6 +896,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       load_v(i, wave);
     }
   }
+  KVQ_STAMP(1);
   // tail key of this wave (if any): lane l holds code byte l of its K and V
   // rows (dims 2l, 2l+1) and the scales of their group
   const int tail_t = t_begin + 64 * ntiles + wave;
@@ -1043,6 +1095,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       const bool masked = ROWMASK || t0 + 64 > t_end;  // wave-uniform
       // ---- QK on the matrix cores: scores of token `lane` for every row ----
       float sc[RS][4];
+      if (i == 0 && base == wave) KVQ_STAMP_AFTER(2, kc4[i][LPT - 1][3]);
       {
         f32x4_t acc[RS][LPT];
 #pragma unroll
@@ -1163,6 +1216,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
       // ---- PV on the matrix cores ----
+      if (i == 0 && base == wave) KVQ_STAMP_AFTER(3, vq[i][NSUB - 1][3]);
       // u = bytes {t0.b, t1.b, t0.b', t1.b'} of two tokens' code dwords; its low
       // and high nibbles then give (token0, token1) pairs of one dim per perm.
 #pragma unroll
@@ -1205,6 +1259,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   //      the half its side of the pair owns. Afterwards the lane of subset g
   //      holds values [g * N / VTS, (g + 1) * N / VTS). Then -> LDS (over the
   //      weight bytes, so every wave must be done with those). ----
+  KVQ_STAMP(4);
   constexpr int NV = 32 * RS;
   float val[NV];
 #pragma unroll
@@ -1268,6 +1323,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   if (new_here) fold_in(new_st, new_v[0], new_v[1]);
   __syncthreads();
   finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
+  KVQ_STAMP(11);
 }
 
 // ===========================================================================
@@ -1711,6 +1767,17 @@ static void launch_d(const AttnArgs& a, const Plan& p, int q_dtype, bool rowmask
 
 }  // namespace kvq
 
+#if defined(KVQ_PHASE_STAMPS)
+// Instrumented builds only: the device buffer the decode launches that follow
+// write their phase stamps to (null: none), [workgroups * 16 * kPhaseSlots]
+// uint64.
+static unsigned long long* g_phase_stamps = nullptr;
+extern "C" int kvq_probe_set_phase_stamps(void* buf) {
+  g_phase_stamps = (unsigned long long*)buf;
+  return 0;
+}
+#endif
+
 using namespace kvq;
 
 extern "C" int64_t kvq_decode_attn_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
@@ -1918,6 +1985,9 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
     while ((int64_t(1) << a.page_shift) < pg->page_size) ++a.page_shift;
   a.pool_rows = pg ? (uint32_t)(pg->n_blocks * pg->page_size) : 0u;
   a.ws_cnt = nullptr; a.ws_ml = nullptr; a.ws_o = nullptr;
+#if defined(KVQ_PHASE_STAMPS)
+  a.stamps = g_phase_stamps;
+#endif
   if (need > 0) {
     char* w = (char*)workspace;
     a.ws_cnt = (uint32_t*)w;

@@ -1,0 +1,121 @@
+// Measurement kernels behind `bench.py --stream-probe` (not part of the
+// decode path's C ABI): a plain streaming read, the ceiling a kernel that only
+// reads a decode step's bytes reaches on this GPU, with and without per-wave
+// clock stamps. Built with the phase-stamped decode kernels into
+// libkvq_probe.so.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvq_probe {
+
+// Thread t reads the 16-byte pieces t, t + T, ..., t + (PER - 1) T of the
+// buffer (T = threads in the grid; pieces past n16 are skipped), all issued
+// before the first is used, and folds them with XOR. Nothing is written
+// unless the fold equals a value no test buffer produces, so the kernel's
+// traffic is the buffer's bytes.
+template <int PER>
+__global__ __launch_bounds__(1024) void stream_read(const uint4* __restrict__ p, uint64_t n16, uint32_t* sink) {
+  const uint64_t t = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
+  const uint64_t T = (uint64_t)gridDim.x * blockDim.x;
+  uint4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint64_t j = t + i * T;
+    v[i] = j < n16 ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+// The same read with per-wave stamps of the 100 MHz s_memrealtime clock:
+// st[(block * 16 + wave) * 4 + k], k = 0 entry, 1 loads issued, 2 first piece
+// arrived, 3 every piece arrived. blockDim.x <= 1024.
+template <int PER>
+__global__ __launch_bounds__(1024) void stream_read_stamped(const uint4* __restrict__ p, uint64_t n16,
+                                                            uint32_t* sink, uint64_t* st) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  const uint64_t t = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
+  const uint64_t T = (uint64_t)gridDim.x * blockDim.x;
+  uint4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint64_t j = t + i * T;
+    v[i] = j < n16 ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  asm volatile("" ::: "memory");
+  const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+  asm volatile("" ::"v"(v[0].x));
+  const uint64_t t2 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  asm volatile("" ::"v"(acc));
+  const uint64_t t3 = __builtin_amdgcn_s_memrealtime();
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+  if ((threadIdx.x & 63) == 0) {
+    uint64_t* s = st + ((uint64_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 4;
+    s[0] = t0;
+    s[1] = t1;
+    s[2] = t2;
+    s[3] = t3;
+  }
+}
+
+typedef void (*read_fn)(const uint4*, uint64_t, uint32_t*);
+typedef void (*read_st_fn)(const uint4*, uint64_t, uint32_t*, uint64_t*);
+
+#define KVQ_PROBE_PERS(X) X(1) X(2) X(3) X(4) X(5) X(6) X(8) X(10) X(12) X(16) X(19) X(20) X(24) X(32) X(37) X(40)
+
+static read_fn pick(int per) {
+#define KVQ_PROBE_CASE(n) \
+  if (per == n) return stream_read<n>;
+  KVQ_PROBE_PERS(KVQ_PROBE_CASE)
+#undef KVQ_PROBE_CASE
+  return nullptr;
+}
+
+static read_st_fn pick_stamped(int per) {
+#define KVQ_PROBE_CASE(n) \
+  if (per == n) return stream_read_stamped<n>;
+  KVQ_PROBE_PERS(KVQ_PROBE_CASE)
+#undef KVQ_PROBE_CASE
+  return nullptr;
+}
+
+// Pieces per thread for a grid: the smallest instantiated count that covers
+// the buffer, or 0 if none does.
+static int pieces_per_thread(uint64_t n16, int grid, int block) {
+  const uint64_t T = (uint64_t)grid * block;
+  const uint64_t need = (n16 + T - 1) / T;
+  static const int pers[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 19, 20, 24, 32, 37, 40};
+  for (int p : pers)
+    if ((uint64_t)p >= need) return p;
+  return 0;
+}
+
+}  // namespace kvq_probe
+
+// One streaming read of `bytes` (a multiple of 16) at buf, grid x block
+// threads; sink holds >= grid uint32. stamps (may be null): per-wave clock
+// stamps, [grid * 16 * 4] uint64, block <= 1024. Returns the pieces per
+// thread used, 0 if no instantiation covers the buffer (nothing launched),
+// -1 on bad arguments or a launch error.
+extern "C" int kvq_probe_stream_read(const void* buf, int64_t bytes, int grid, int block, void* sink,
+                                     void* stamps, void* stream) {
+  if (buf == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || grid <= 0 || block <= 0 ||
+      block > 1024 || block % 64 != 0)
+    return -1;
+  const uint64_t n16 = (uint64_t)bytes / 16;
+  const int per = kvq_probe::pieces_per_thread(n16, grid, block);
+  if (per == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (stamps != nullptr)
+    hipLaunchKernelGGL(kvq_probe::pick_stamped(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
+                       (uint32_t*)sink, (uint64_t*)stamps);
+  else
+    hipLaunchKernelGGL(kvq_probe::pick(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
+                       (uint32_t*)sink);
+  return hipGetLastError() == hipSuccess ? per : -1;
+}

@@ -43,21 +43,52 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+# The measurement library behind bench.py --stream-probe: the streaming-read
+# probe kernels and the decode kernels built with phase stamps.
+PROBE_OUT = os.path.join(_HERE, "libkvq_probe.so")
+PROBE_SOURCES = (("probe/kvq_probe.hip", ()), ("kvq_attn.hip", ("-DKVQ_PHASE_STAMPS=1",)), ("kvq_capi.hip", ()))
+
+
+def _build_libs(libs, verbose: bool) -> None:
+    """libs: [(output path, [(source under csrc, extra flags)])]. Every
+    object compiles in parallel, then each library links."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    tmpdir = tempfile.mkdtemp(prefix="kvint4-build.", dir=_HERE)
+    try:
+        compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+        jobs = []
+        for li, (_, srcs) in enumerate(libs):
+            for si, (s, extra) in enumerate(srcs):
+                jobs.append((os.path.join(CSRC, s), list(extra), os.path.join(tmpdir, f"{li}_{si}.o")))
+
+        def compile_one(job) -> None:
+            src, extra, obj = job
+            cmd = [hipcc(), *compile_flags, *extra, "-c", src, "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            proc = subprocess.run(cmd, capture_output=True, text=True)
+            if proc.returncode != 0:
+                raise RuntimeError(f"hipcc failed ({proc.returncode}) on {src}:\n{proc.stdout}\n{proc.stderr}")
+
+        with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+            list(ex.map(compile_one, jobs))
+        for li, (out, srcs) in enumerate(libs):
+            objs = [os.path.join(tmpdir, f"{li}_{si}.o") for si in range(len(srcs))]
+            tmp = os.path.join(tmpdir, os.path.basename(out))
+            cmd = [hipcc(), *HIPCC_FLAGS, *objs, "-o", tmp]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            proc = subprocess.run(cmd, capture_output=True, text=True)
+            if proc.returncode != 0:
+                raise RuntimeError(f"hipcc link failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+            os.replace(tmp, out)  # atomic: a reader never sees a half-written library
+    finally:
+        shutil.rmtree(tmpdir, ignore_errors=True)
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every HIP source into kvint4/libkvint4.so; return its path."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    fd, tmp = tempfile.mkstemp(prefix="libkvint4.", suffix=".so.tmp", dir=_HERE)
-    os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        os.unlink(tmp)
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, OUT)  # atomic: a reader never sees a half-written library
+    """Compile every HIP source into kvint4/libkvint4.so (the product) and
+    kvint4/libkvq_probe.so (measurement only); return the product's path."""
+    _build_libs([(OUT, [(s, ()) for s in SOURCES]), (PROBE_OUT, list(PROBE_SOURCES))], verbose)
     return OUT
-
-
-if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
