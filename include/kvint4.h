@@ -196,6 +196,35 @@ int kvq_decode_step(const void* q, int q_dtype, const int64_t* q_strides,
                     void* stream);
 
 /*
+ * kvq_decode_step_noalloc — kvq_decode_step with no workspace argument: the
+ * split partials and counters go to a 4 MiB array of device memory that the
+ * library holds per GPU (a static device array, looked up once per device),
+ * so the call allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).
+ *
+ * Arguments, results and errors as kvq_decode_step without workspace /
+ * workspace_bytes. A plan whose workspace (kvq_decode_attn_workspace_bytes)
+ * exceeds 4 MiB is refused with KVQ_ESPACE before any device call. Every call
+ * on one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * race (serialize them, e.g. one stream); consecutive calls need nothing in
+ * between (each leaves the array ready for the next).
+ */
+int kvq_decode_step_noalloc(const void* q, int q_dtype, const int64_t* q_strides,
+                            const void* k_new, const int64_t* kn_strides,
+                            const void* v_new, const int64_t* vn_strides,
+                            void* k_packed, const int64_t* kp_strides,
+                            void* k_scales, const int64_t* ks_strides,
+                            void* v_packed, const int64_t* vp_strides,
+                            void* v_scales, const int64_t* vs_strides,
+                            int scale_dtype,
+                            void* out, const int64_t* out_strides,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                            int64_t group_size, int64_t capacity,
+                            const int32_t* positions, int64_t pos0, float sm_scale,
+                            int64_t n_split, void* stream);
+
+/*
  * kvq_prefill_attn — attention of a long query block (prompt prefill, or a
  * prompt chunk after cached tokens) over an INT4 cache, on the matrix cores.
  * Replaces the reference's fused GQA kernel at Sq > 1

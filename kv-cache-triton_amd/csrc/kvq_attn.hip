@@ -46,6 +46,7 @@
 // Softmax runs in base 2 with sm_scale*log2(e) folded into the key scale.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "kvq_common.h"
@@ -2152,4 +2153,86 @@ extern "C" int kvq_decode_step_paged(const void* q, int q_dtype, const int64_t* 
                           k_scale_pool, ks.v, v_pool, vp.v, v_scale_pool, vs.v, scale_dtype, out,
                           out_strides, B, Hq, Hkv, D, group_size, table_cols * page_size, positions, pos0,
                           sm_scale, n_split, workspace, workspace_bytes, stream, &pg);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode step: the split workspace is a file-scope device
+// array, not a caller buffer, for callers that cannot allocate (code under
+// HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+
+namespace {
+constexpr int64_t kScratchBytes = 4ll << 20;  // the largest split workspace a call may need
+constexpr int kScratchDevices = 64;
+}  // namespace
+
+// One copy per GPU the library runs on, held until the process ends. It is
+// zero at load, and every completed call leaves its counter block at zero
+// again (the merging workgroup re-arms each counter it used), so no call
+// clears it; the partials need no initialisation.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current. (The array's name in host code is a
+// host-side handle, not a device address.)
+static int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    kvq::set_error("kvq_decode_step_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return KVQ_EHIP;
+  }
+  if (dev < 0 || dev >= kScratchDevices) {
+    kvq::set_error("kvq_decode_step_noalloc: device %d beyond the %d devices with a scratch slot", dev,
+                   kScratchDevices);
+    return KVQ_EUNSUP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      kvq::set_error("kvq_decode_step_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                     hipGetErrorString(e));
+      return KVQ_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KVQ_OK;
+}
+
+extern "C" int kvq_decode_step_noalloc(const void* q, int q_dtype, const int64_t* q_strides,
+                                       const void* k_new, const int64_t* kn_strides,
+                                       const void* v_new, const int64_t* vn_strides,
+                                       void* k_packed, const int64_t* kp_strides,
+                                       void* k_scales, const int64_t* ks_strides,
+                                       void* v_packed, const int64_t* vp_strides,
+                                       void* v_scales, const int64_t* vs_strides,
+                                       int scale_dtype,
+                                       void* out, const int64_t* out_strides,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                       int64_t group_size, int64_t capacity,
+                                       const int32_t* positions, int64_t pos0, float sm_scale,
+                                       int64_t n_split, void* stream) {
+  kvq::clear_error();
+  const int64_t need = kvq_decode_attn_workspace_bytes(B, Hq, Hkv, 1, D, q_dtype, scale_dtype, n_split);
+  if (need < 0) return (int)need;  // the planner set the message
+  if (need > kScratchBytes) {
+    kvq::set_error("kvq_decode_step_noalloc: the split plan needs %lld workspace bytes, more than the "
+                   "%lld-byte static scratch (use kvq_decode_step with a workspace, or fewer splits)",
+                   (long long)need, (long long)kScratchBytes);
+    return KVQ_ESPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_on_current_device(&ws);
+    if (rc != KVQ_OK) return rc;
+  }
+  return decode_step_impl(q, q_dtype, q_strides, k_new, kn_strides, v_new, vn_strides, k_packed,
+                          kp_strides, k_scales, ks_strides, v_packed, vp_strides, v_scales, vs_strides,
+                          scale_dtype, out, out_strides, B, Hq, Hkv, D, group_size, capacity, positions, pos0,
+                          sm_scale, n_split, ws, need > 0 ? kScratchBytes : 0, stream, nullptr);
 }

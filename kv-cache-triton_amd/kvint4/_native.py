@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_attn_workspace_bytes",
     "kvq_decode_attn",
     "kvq_decode_step",
+    "kvq_decode_step_noalloc",
     "kvq_quantize_paged",
     "kvq_dequantize_paged",
     "kvq_decode_attn_paged",
@@ -92,6 +93,17 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, ctypes.c_float,
         _i64, _vp, _i64, _vp,
+    ]
+    lib.kvq_decode_step_noalloc.restype = _i32
+    lib.kvq_decode_step_noalloc.argtypes = [
+        _vp, _i32, _i64p,
+        _vp, _i64p, _vp, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _i32,
+        _vp, _i64p,
+        _i64, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, ctypes.c_float,
+        _i64, _vp,
     ]
     lib.kvq_prefill_attn_workspace_bytes.restype = _i64
     lib.kvq_prefill_attn_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64]

@@ -146,3 +146,23 @@ def test_prefill_entry_points_validate_before_any_launch():
     assert lib.kvq_prefill_attn_workspace_bytes(1, 32, 8, 16384, 128, 16384) == 0
     assert lib.kvq_prefill_attn_workspace_bytes(0, 32, 8, 128, 128, 16384) == 0
     assert lib.kvq_prefill_attn_workspace_bytes(1, 32, 8, 128, 96, 16384) == nat.KVQ_EINVAL
+
+
+def test_noalloc_step_refuses_plans_beyond_its_scratch():
+    """kvq_decode_step_noalloc: a split plan whose workspace exceeds the 4 MiB
+    static scratch is refused with KVQ_ESPACE before any device call (null
+    tensors are never read), and planner errors pass through."""
+    lib = nat.lib()
+    B16 = nat.KVQ_BF16
+    s4 = nat.i64_array([0, 0, 0, 1])
+    s3 = nat.i64_array([0, 0, 0])
+
+    def call(B, Hkv, n_split, D=128):
+        return lib.kvq_decode_step_noalloc(None, B16, s4, None, s4, None, s4, None, s3, None, s3, None, s3,
+                                           None, s3, B16, None, s4, B, 8 * Hkv, Hkv, D, 32, 4097, None, 4096,
+                                           0.1, n_split, None)
+
+    need = lib.kvq_decode_attn_workspace_bytes(64, 64, 8, 1, 128, B16, B16, 4)
+    assert need > 4 << 20
+    assert call(64, 8, 4) == nat.KVQ_ESPACE and "static scratch" in nat.last_error()
+    assert call(1, 8, 4, D=96) == nat.KVQ_EUNSUP
