@@ -438,9 +438,13 @@ def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
     n = -(-nbytes // 16) * 16
     g = torch.Generator(device=dev).manual_seed(7)
     bufs = [torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev, generator=g) for _ in range(L)]
-    sink = torch.zeros(max(gr for gr, _ in grids), dtype=torch.int32, device=dev)
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)  # >= any grid below (one word per workgroup)
     out = []
     for grid, block in grids:
+        # larger buffers: more workgroups, so that each thread keeps at most
+        # 20 pieces in flight (no register spills)
+        while -(-(n // 16) // (grid * block)) > 20:
+            grid *= 2
         graph = torch.cuda.CUDAGraph()
         per = 0
         with torch.cuda.graph(graph, stream=stream):

@@ -31,11 +31,16 @@ DEV = torch.device("cuda:0")
 TDT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 
 
-def _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, seed, scale_dtype=None, G=32):
+def _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, seed, scale_dtype=None, G=32, outliers=()):
+    """Seeded ~N(0, 1) q, K, V (K channels listed in `outliers` scaled x8),
+    K and V quantized on the GPU."""
     g = torch.Generator().manual_seed(seed)
     t = TDT[dtype]
     q = torch.randn(B, Hq, Sq, D, generator=g).to(t)
-    k = torch.randn(B, Hkv, Sk, D, generator=g).to(t)
+    k = torch.randn(B, Hkv, Sk, D, generator=g)
+    if len(outliers):
+        k[..., list(outliers)] *= 8.0
+    k = k.to(t)
     v = torch.randn(B, Hkv, Sk, D, generator=g).to(t)
     sd = scale_dtype or dtype
     kp, ks = ops.quantize(k.to(DEV), G, TDT[sd])
@@ -95,13 +100,23 @@ def test_decode_matches_oracle(B, Hq, Hkv, Sk, D, G, dtype):
     assert err_w <= 2e-2, f"vs as-written oracle: {err_w}"
 
 
+# eight fixed head-dim channels of K scaled x8 (the Llama decode configuration's outliers)
+OUTLIER_CHANNELS = (3, 17, 29, 46, 64, 81, 100, 122)
+
+
 def test_north_star_shape_16k():
-    q, kp, ks, vp, vs = _inputs(1, 32, 8, 1, 16384, 128, "bf16", seed=16)
-    # 8 outlier key channels (x8), as in the Llama decode config
+    """Llama-3.1-8B decode shape at 16K keys with eight x8 outlier key
+    channels, against both oracles (float64 over the exact dequantized
+    values, and the reference's as-written bf16 dequantize -> SDPA)."""
+    q, kp, ks, vp, vs = _inputs(1, 32, 8, 1, 16384, 128, "bf16", seed=16, outliers=OUTLIER_CHANNELS)
     out = attention_forward_quant_gqa(q.to(DEV), kp, ks, vp, vs, n_q_heads=32, n_kv_heads=8)
     got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
     err = np.abs(got - _oracle(q, kp, ks, vp, vs, 32)).max()
-    assert err <= 2e-2, err
+    err_w = np.abs(got - _as_written(q, kp, ks, vp, vs, 32, 4)).max()
+    print(f"NS 16K with outliers: max-abs vs float64 oracle {err:.2e}, vs as-written oracle {err_w:.2e}")
+    assert err <= 2e-2, f"vs float64 oracle: {err}"
+    assert err_w <= 2e-2, f"vs as-written oracle: {err_w}"
 
 
 @pytest.mark.parametrize("Sk", [1, 64, 1024, 3000])
