@@ -422,6 +422,9 @@ def probe_lib():
     lib.kvq_probe_stream_read.restype = ctypes.c_int
     lib.kvq_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.kvq_probe_stream_read_padded.restype = ctypes.c_int
+    lib.kvq_probe_stream_read_padded.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_void_p, ctypes.c_void_p]
     lib.kvq_probe_set_phase_stamps.restype = ctypes.c_int
     lib.kvq_probe_set_phase_stamps.argtypes = [ctypes.c_void_p]
     return lib
@@ -532,6 +535,32 @@ def stream_probe_bench(args, w: dict) -> int:
     t0 = s[:, 0].min()
     names = ("entry", "loads_issued", "first_arrived", "all_arrived")
     stream_phases = {nm: _dist((s[:, k] - t0) * 10.0) for k, nm in enumerate(names)}
+
+    # issue cost: the same read (grid 256 x 512, 10 pieces per thread) with N
+    # dependent VALU instructions before (or after) its loads
+    issue = []
+    if n <= 256 * 512 * 10 * 16:
+        for pad, after in ((0, 0), (256, 0), (512, 0), (1024, 0), (2048, 0), (512, 1), (2048, 1)):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for b in keep:
+                    rc = lib.kvq_probe_stream_read_padded(b.data_ptr(), n, pad, after, sink.data_ptr(),
+                                                          stream.cuda_stream)
+            if rc != 0:
+                continue
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    graph.replay()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(20):
+                    graph.replay()
+                e1.record(stream)
+            torch.cuda.synchronize()
+            issue.append({"valu_instructions": pad, "placed": "after loads" if after else "before loads",
+                          "us_per_launch": round(e0.elapsed_time(e1) * 1e3 / (20 * len(keep)), 3)})
     del keep
 
     # the decode step: product kernel timing, then the instrumented build's phases
@@ -611,6 +640,7 @@ def stream_probe_bench(args, w: dict) -> int:
         "workload": w["desc"], "bytes_per_launch": nbytes, "layers": L,
         "stream": stream_rows, "best": best,
         "stream_phases_ns": dict(stream_phases, grid=grid, block=block),
+        "issue_cost": issue,
         "decode_step": {"us_per_launch": round(dec_us, 3), "gbs": round(dec_bytes / (dec_us * 1e-6) / 1e9, 1),
                         "frac_of_peak": round(dec_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                         "frac_of_best_read": round(best["us_per_launch"] / dec_us, 4), "n_split": int(ns)},

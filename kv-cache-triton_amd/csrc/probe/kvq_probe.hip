@@ -63,6 +63,35 @@ __global__ __launch_bounds__(1024) void stream_read_stamped(const uint4* __restr
   }
 }
 
+// The read of stream_read<10> with N dependent v_add instructions (8 bytes
+// each) before its loads (AFTER = false) or after them: what one instruction
+// on a wave's path to its first load costs when two waves share a SIMD.
+template <int N, bool AFTER>
+__global__ __launch_bounds__(512) void stream_read_padded(const uint4* __restrict__ p, uint64_t n16, uint32_t* sink) {
+  constexpr int PER = 10;
+  const uint64_t t = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
+  const uint64_t T = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t x = threadIdx.x;
+  if (!AFTER) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("v_add_u32 %0, 0x12345, %0" : "+v"(x));
+  }
+  uint4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint64_t j = t + i * T;
+    v[i] = j < n16 ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  if (AFTER) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("v_add_u32 %0, 0x12345, %0" : "+v"(x));
+  }
+  uint32_t acc = x;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
 typedef void (*read_fn)(const uint4*, uint64_t, uint32_t*);
 typedef void (*read_st_fn)(const uint4*, uint64_t, uint32_t*, uint64_t*);
 
@@ -118,4 +147,23 @@ extern "C" int kvq_probe_stream_read(const void* buf, int64_t bytes, int grid, i
     hipLaunchKernelGGL(kvq_probe::pick(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
                        (uint32_t*)sink);
   return hipGetLastError() == hipSuccess ? per : -1;
+}
+
+// stream_read_padded over `bytes` (a multiple of 16, at most 256 * 512 * 10 * 16
+// bytes) with grid 256 x 512: pad in {0, 256, 512, 1024, 2048}, after != 0
+// places the instructions after the loads. Returns 0, or -1 on bad arguments
+// or a launch error.
+extern "C" int kvq_probe_stream_read_padded(const void* buf, int64_t bytes, int pad, int after, void* sink,
+                                            void* stream) {
+  using namespace kvq_probe;
+  if (buf == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || bytes > 256ll * 512 * 10 * 16) return -1;
+  read_fn f = nullptr;
+#define KVQ_PAD_CASE(n)                                                              \
+  if (pad == n) f = after ? stream_read_padded<n, true> : stream_read_padded<n, false>;
+  KVQ_PAD_CASE(0) KVQ_PAD_CASE(256) KVQ_PAD_CASE(512) KVQ_PAD_CASE(1024) KVQ_PAD_CASE(2048)
+#undef KVQ_PAD_CASE
+  if (f == nullptr) return -1;
+  hipLaunchKernelGGL(f, dim3(256), dim3(512), 0, (hipStream_t)stream, (const uint4*)buf, (uint64_t)bytes / 16,
+                     (uint32_t*)sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
