@@ -9,7 +9,8 @@ model (embedding, 32 decoder layers with one fused append + attention launch
 each, norm, LM head, argmax) is captured once into a HIP graph and replayed:
 
   * the cache keeps its write positions in device memory (``make_static``),
-    and the captured step advances them in place;
+    and the captured step advances them in place; a paged cache also takes
+    the blocks of every step and uploads its block table before capture;
   * position ids, the input token and the step counter are device tensors
     that the step also updates in place, so each replay feeds the next;
   * generated tokens are written into a device [B, max_new_tokens] buffer;
@@ -40,6 +41,7 @@ from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
 from .. import ops
 from ..cache_base import QuantizedKVCacheBase
+from ..paged_cache import PagedQuantizedKVCache
 from .llama3_quant import LlamaAttentionQuantized
 
 
@@ -74,9 +76,11 @@ class GraphedGreedyDecoder:
 
     model          a Llama causal LM whose attention modules were swapped by
                    ``replace_llama_attention_with_quantized``.
-    cache          the contiguous ``QuantizedKVCache`` the prompt was
-                   prefilled into (every sequence of the batch the same
-                   length: the decode step runs without a mask).
+    cache          the ``QuantizedKVCache`` or ``PagedQuantizedKVCache`` the
+                   prompt was prefilled into (every sequence of the batch the
+                   same length: the decode step runs without a mask). A paged
+                   cache gets its blocks for every step now (``make_static``),
+                   so the captured step allocates and copies nothing.
     next_token     [B, 1] int64 device tensor: the token after the prompt
                    (argmax of the prefill's last logits), fed to step 0.
     warmup_steps   eager steps run before capture (they are real steps: their
@@ -90,8 +94,8 @@ class GraphedGreedyDecoder:
 
     def __init__(self, model, cache: QuantizedKVCacheBase, next_token: torch.Tensor,
                  max_new_tokens: int, warmup_steps: int = 2):
-        if not isinstance(cache, QuantizedKVCacheBase):
-            raise TypeError("GraphedGreedyDecoder needs the contiguous QuantizedKVCache")
+        if not isinstance(cache, (QuantizedKVCacheBase, PagedQuantizedKVCache)):
+            raise TypeError("GraphedGreedyDecoder needs a QuantizedKVCache or a PagedQuantizedKVCache")
         attn = [m for m in model.modules() if isinstance(m, LlamaAttentionQuantized)]
         if not attn:
             raise ValueError("the model's attention modules are not LlamaAttentionQuantized "

@@ -74,6 +74,7 @@ class PagedQuantizedKVCache:
         self._table: Optional[torch.Tensor] = None
         self._table_dirty = False
         self._shape: Optional[tuple] = None             # (B, H, D, x dtype, scale dtype, device)
+        self.fused_steps = 0  # append_and_attend calls served by the one-launch decode step
 
     def _setup(self, x: torch.Tensor) -> None:
         B, H, _, D = x.shape
@@ -290,7 +291,63 @@ class PagedQuantizedKVCache:
             return None
         pos.add_(1)
         self._lens[layer_idx] = [n + 1 for n in lens]
+        self.fused_steps += 1
         return out
+
+    # -- decode steps captured in a HIP graph --------------------------------
+    def make_static(self, extra_tokens: int) -> None:
+        """Prepare every layer for decode steps captured in a HIP graph.
+
+        A replay cannot allocate, copy blocks or upload a table, and it keeps
+        the pools and the table it was captured with. So every sequence gets
+        its blocks for `extra_tokens` more positions now (the pools grow now
+        if they must), every block in those positions that sequences share
+        (after a beam reorder or a batch repeat) is copied to its own block
+        now, and the table is uploaded once. A captured decode step then finds
+        nothing to allocate, copy or upload; its write positions are the
+        layers' device lengths, which it advances in place.
+
+        The Python-side lengths (``get_seq_length``) are not touched by a replay.
+        Whoever replays advances them with ``advance_host_lengths``."""
+        extra_tokens = int(extra_tokens)
+        if extra_tokens < 0:
+            raise ValueError("extra_tokens must be >= 0")
+        if not self._pools or self._shape is None:
+            raise ValueError("make_static needs a prefilled cache (no layer holds tokens)")
+        B = self._shape[0]
+        lo = [min(lens[b] for lens in self._lens.values()) for b in range(B)]
+        hi = [max(lens[b] for lens in self._lens.values()) + extra_tokens for b in range(B)]
+        self._ensure_pages(hi)
+        self._make_writable(lo, [h - l for h, l in zip(hi, lo)])
+        self._page_table()
+
+    def buffer_signature(self) -> tuple:
+        """Device addresses a HIP graph captured over this cache holds: the
+        block table and every layer's pools and device lengths. An edit that
+        replaces one (pool growth, a table re-upload after new or copied
+        blocks) changes the signature."""
+        table = None if self._table is None else (self._table.data_ptr(), tuple(self._table.shape))
+        return (table, self._num_blocks) + tuple(
+            (i, *(t.data_ptr() for t in pools), self._seq_lens[i].data_ptr())
+            for i, pools in sorted(self._pools.items())
+        )
+
+    def host_lengths(self) -> dict[int, int]:
+        """Python-side length of every layer, for a batch whose sequences all
+        have one length (the graph decoder's case); raises otherwise."""
+        out = {}
+        for i, lens in self._lens.items():
+            if len(set(lens)) > 1:
+                raise ValueError(f"layer {i}: the sequences' lengths differ ({sorted(set(lens))})")
+            out[i] = int(lens[0]) if lens else 0
+        return out
+
+    def advance_host_lengths(self, base: dict[int, int], n: int) -> None:
+        """Set each layer's Python-side length of every sequence to base[layer]
+        + n: the bookkeeping of n decode steps that ran as graph replays (the
+        device lengths were advanced by the replays themselves)."""
+        for i in self._lens:
+            self._lens[i] = [int(base[i]) + int(n)] * len(self._lens[i])
 
     # -- attention -----------------------------------------------------------
     def attend(self, query_states: torch.Tensor, layer_idx: int, *, n_kv_heads: int, scale: float,

@@ -13,7 +13,10 @@ eager logits to within twice that step's difference, and 99 % of the cache
 bytes equal (a code moves where the projected K/V round differently). The replays are interleaved with unrelated eager work and host
 synchronisations. Plain eager decoding (host write positions, a split plan
 sized to the context) is compared on the logits of the first step, within
-the attention bar."""
+the attention bar. Caches: contiguous; paged (pages of 64, the table grown
+and uploaded by make_static before capture); and paged with the batch's
+sequences sharing their prompt blocks (batch_repeat_interleave), which
+make_static copies apart before capture."""
 
 from __future__ import annotations
 
@@ -24,6 +27,7 @@ from transformers import LlamaConfig, LlamaForCausalLM
 from kvint4.llama3.graph_decode import GraphedGreedyDecoder
 from kvint4.llama3.kv_cache import QuantizedKVCache
 from kvint4.llama3.llama3_quant import replace_llama_attention_with_quantized
+from kvint4.paged_cache import PagedQuantizedKVCache
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -47,21 +51,38 @@ def _model(head_dim: int):
     return model
 
 
-def _prefill(model, prompt):
-    cache = QuantizedKVCache(group_size=32)
+def _prefill(model, prompt, kind="contiguous"):
+    """Prefill a fresh cache. kind: "contiguous", "paged" (pages of 64), or
+    "shared" (paged; the batch's first prompt prefilled once and repeated
+    with batch_repeat_interleave, so the sequences share their blocks)."""
+    if kind == "contiguous":
+        cache = QuantizedKVCache(group_size=32)
+    else:
+        cache = PagedQuantizedKVCache(group_size=32, page_size=64)
+    B = prompt.shape[0]
     with torch.no_grad():
-        out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
-    return cache, out.logits[:, -1].float(), out.logits[:, -1].argmax(-1, keepdim=True)
+        if kind == "shared":
+            out = model(input_ids=prompt[:1], past_key_values=cache, use_cache=True, logits_to_keep=1)
+            cache.batch_repeat_interleave(B)
+            logits = out.logits[:, -1].repeat(B, 1)
+        else:
+            out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            logits = out.logits[:, -1]
+    return cache, logits.float(), logits.argmax(-1, keepdim=True)
 
 
-@pytest.mark.parametrize("head_dim,B,prompt_len,steps", [(64, 2, 70, 12), (128, 1, 300, 10)])
-def test_graph_replays_match_eager_steps(head_dim, B, prompt_len, steps):
-    print(f"graph decode: head_dim {head_dim}, batch {B}, prompt {prompt_len}, steps {steps}", flush=True)
+@pytest.mark.parametrize("head_dim,B,prompt_len,steps,kind", [
+    (64, 2, 70, 12, "contiguous"), (128, 1, 300, 10, "contiguous"),
+    (128, 2, 300, 40, "paged"), (64, 2, 100, 12, "shared"),
+])
+def test_graph_replays_match_eager_steps(head_dim, B, prompt_len, steps, kind):
+    print(f"graph decode: head_dim {head_dim}, batch {B}, prompt {prompt_len}, steps {steps}, {kind} cache",
+          flush=True)
     model = _model(head_dim)
     prompt = torch.randint(0, 512, (B, prompt_len), generator=torch.Generator().manual_seed(5)).to(DEV)
 
     # graph replays, with unrelated eager work between them
-    cache_g, _, nxt_g = _prefill(model, prompt)
+    cache_g, _, nxt_g = _prefill(model, prompt, kind)
     warm = 2
     dec = GraphedGreedyDecoder(model, cache_g, nxt_g, max_new_tokens=steps, warmup_steps=warm)
     junk = torch.randn(256, 256, device=DEV)
@@ -78,7 +99,7 @@ def test_graph_replays_match_eager_steps(head_dim, B, prompt_len, steps):
 
     # eager steps over a cache in the same device-length mode, fed the graph's
     # tokens (teacher forcing)
-    cache_e, _, nxt = _prefill(model, prompt)
+    cache_e, _, nxt = _prefill(model, prompt, kind)
     assert torch.equal(nxt, nxt_g)
     cache_e.make_static(steps)
     pos = torch.full((B, 1), prompt_len, dtype=torch.int64, device=DEV)
@@ -119,10 +140,10 @@ def test_graph_replays_match_eager_steps(head_dim, B, prompt_len, steps):
     # the context, not to the capacity, so the attention rounds differently
     # (each within the attention bar of the oracle, tests/test_gpu_decode_step.py);
     # the two layers carry that to the first step's logits
-    cache_p, _, nxt_p = _prefill(model, prompt)
+    cache_p, _, nxt_p = _prefill(model, prompt, kind)
     with torch.no_grad():
         out = model(input_ids=nxt_p, past_key_values=cache_p, use_cache=True, logits_to_keep=1)
-        cache_s, _, _ = _prefill(model, prompt)
+        cache_s, _, _ = _prefill(model, prompt, kind)
         cache_s.make_static(1)
         ref = model(input_ids=nxt_p, position_ids=torch.full((B, 1), prompt_len, device=DEV),
                     past_key_values=cache_s, use_cache=True, logits_to_keep=1)

@@ -208,7 +208,64 @@ def test_graph_decoder_rejects_unswapped_models_and_other_caches():
     with pytest.raises(ValueError, match="replace_llama_attention_with_quantized"):
         GraphedGreedyDecoder(model, QuantizedKVCache(), tok, max_new_tokens=4)
     with pytest.raises(TypeError):
-        GraphedGreedyDecoder(model, PagedQuantizedKVCache(), tok, max_new_tokens=4)
+        GraphedGreedyDecoder(model, object(), tok, max_new_tokens=4)
+    del PagedQuantizedKVCache
+
+
+def test_paged_make_static_takes_blocks_unshares_them_and_fixes_the_table(monkeypatch):
+    """PagedQuantizedKVCache.make_static (host bookkeeping, CPU pools; the
+    table holder's device check is lifted for the test): the blocks for the
+    extra positions are taken now, a block two sequences share inside that
+    range gets a private copy, the table is uploaded once, and later
+    decode-step bookkeeping finds nothing to allocate or copy."""
+    from kvint4.paged_cache import PagedQuantizedKVCache
+
+    class HostTable:
+        def __init__(self, table, page_size, num_blocks):
+            self.table, self.page_size, self.num_blocks = table, page_size, num_blocks
+
+    monkeypatch.setattr(ops, "PageTable", HostTable)
+
+    c = PagedQuantizedKVCache(group_size=32, page_size=64)
+    with pytest.raises(ValueError):
+        c.make_static(4)
+    c._setup(torch.zeros(1, 2, 1, 64, dtype=torch.bfloat16))  # B=1, 2 KV heads, d_head 64
+    for i in (0, 1):
+        c._layer(i)
+    c._ensure_pages([100])                                     # 2 blocks
+    c._lens = {0: [100], 1: [100]}
+    for i in (0, 1):
+        c._seq_lens[i].fill_(100)
+        for t in c._pools[i]:
+            t.copy_(torch.arange(t.numel()).view(t.shape).to(t.dtype))
+    c.batch_repeat_interleave(2)                               # both sequences share both blocks
+    assert c._pages[0] == c._pages[1] and all(c._ref[b] == 2 for b in c._pages[0])
+    shared_last = c._pages[0][1]
+    before = [t.clone() for t in c.get_quantized(0)]
+    c.make_static(60)                                          # positions 100..159: pages 1 and 2
+    assert len(c._pages[0]) == 3 and len(c._pages[1]) == 3
+    assert c._pages[0][0] == c._pages[1][0]                   # page 0 is not written: still shared
+    assert c._pages[0][1] != c._pages[1][1]                   # page 1 is written: copied apart
+    assert all(c._ref[c._pages[b][i]] == 1 for b in (0, 1) for i in (1, 2))
+    assert shared_last in (c._pages[0][1], c._pages[1][1])
+    for a, b in zip(before, c.get_quantized(0)):               # the stored rows are unchanged
+        assert torch.equal(a, b)
+    sig = c.buffer_signature()
+    table = c.block_table()
+    # what a captured decode step does on the host: nothing to allocate, copy or upload
+    lens = c._lens[0]
+    c._ensure_pages([n + 1 for n in lens])
+    c._make_writable(lens, 1)
+    assert not c._table_dirty and c.block_table() is table and c.buffer_signature() == sig
+    base = c.host_lengths()
+    assert base == {0: 100, 1: 100}
+    c.advance_host_lengths(base, 7)
+    assert c.get_seq_length(0) == 107 and c._lens[1] == [107, 107]
+    c._lens[1] = [107, 106]
+    with pytest.raises(ValueError, match="differ"):
+        c.host_lengths()
+    with pytest.raises(ValueError):
+        c.make_static(-1)
 
 
 def test_workspace_growth_keeps_captured_buffers_alive():
