@@ -642,9 +642,10 @@ __device__ __forceinline__ void chunk_scales(uint2 raw, bool g32, const uint32_t
 
 // D = 64 with one row set fits 128 VGPRs: four waves per SIMD, so two
 // 8-wave workgroups share a CU (a batch of many short sequences then runs
-// in one round of workgroups instead of two).
+// in one round of workgroups instead of two). Two row sets are held to 256
+// registers: two waves per SIMD, one 8-wave workgroup per CU.
 template <int D, int RS>
-constexpr int mfma_waves_per_simd() { return D == 64 && RS == 1 ? 4 : 1; }
+constexpr int mfma_waves_per_simd() { return D == 64 && RS == 1 ? 4 : (RS == 2 ? 2 : 1); }
 
 template <int D, int RS, int QM, int SM, bool ROWMASK, int NW, int CH, bool PAGED>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mfma_waves_per_simd<D, RS>())))
@@ -680,6 +681,15 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
   __shared__ __attribute__((aligned(16))) float ml_lds[NW][ROWS][2];
   __shared__ MergeLds<64 * NW> mg;
+  // With two row sets, values the tile loop does not change are kept in LDS
+  // rather than registers, so that the kernel fits two waves per SIMD: each
+  // wave's accumulator init per (row set, chunk), the same in every lane;
+  // and the decode step's new token (its scores per row, then two
+  // dequantized value elements per lane), folded in after the loop. One row
+  // set has registers to spare and keeps them in registers.
+  constexpr bool KEEP_IN_LDS = RS > 1;
+  __shared__ __attribute__((aligned(16))) float qb_lds[KEEP_IN_LDS ? NW : 1][RS][LPT][4];
+  __shared__ __attribute__((aligned(16))) float nt_lds[KEEP_IN_LDS ? RS * 4 + 128 : 1];
   auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem);
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
@@ -944,7 +954,9 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int my_row = lane & 3;
-  // accumulator init -bias * sum(q) per 32-dim chunk, on the MFMA
+  // accumulator init -bias * sum(q) per 32-dim chunk, on the MFMA (every
+  // lane gets the same four row values; with two row sets lane 0 keeps them
+  // in LDS)
   f32x4_t qinit[RS][LPT];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
@@ -957,8 +969,17 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
         acc = mfma4<F16>(q4.x, q4.y, NEG_BIAS, NEG_BIAS, acc);
         acc = mfma4<F16>(q4.z, q4.w, NEG_BIAS, NEG_BIAS, acc);
       }
-      qinit[rs][c] = acc;
+      if constexpr (KEEP_IN_LDS) {
+        if (lane == 0) *(f32x4_t*)&qb_lds[wave][rs][c][0] = acc;
+      } else {
+        qinit[rs][c] = acc;
+      }
     }
+  }
+  if constexpr (KEEP_IN_LDS) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
   // ---- single keys outside the tile loop (a split's tail keys, a decode
@@ -1069,6 +1090,15 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
     key_scores(deq[0][0], deq[0][1], L, new_st);
     new_v[0] = deq[1][0];
     new_v[1] = deq[1][1];
+    if constexpr (KEEP_IN_LDS) {
+      if (lane == 0) {
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) nt_lds[rs * 4 + r] = new_st[rs][r];
+      }
+      *(float2*)&nt_lds[RS * 4 + 2 * lane] = make_float2(new_v[0], new_v[1]);
+    }
   }
 
   // ---- running softmax state (base 2; scores carry sm_scale * log2 e) ----
@@ -1102,7 +1132,10 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-          for (int c = 0; c < LPT; ++c) acc[rs][c] = qinit[rs][c];
+          for (int c = 0; c < LPT; ++c) {
+            if constexpr (KEEP_IN_LDS) acc[rs][c] = *(const f32x4_t*)&qb_lds[wave][rs][c][0];
+            else acc[rs][c] = qinit[rs][c];
+          }
 #pragma unroll
         for (int c = 0; c < LPT; ++c) {
 #pragma unroll
@@ -1321,7 +1354,21 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
                tail_t, st);
     fold_in(st, ((float)(int)(tail_vb & 15u) - 8.0f) * vsf, ((float)(int)((tail_vb >> 4) & 15u) - 8.0f) * vsf);
   }
-  if (new_here) fold_in(new_st, new_v[0], new_v[1]);
+  if (new_here) {
+    if constexpr (KEEP_IN_LDS) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) new_st[rs][r] = nt_lds[rs * 4 + r];
+      const float2 nv = *(const float2*)&nt_lds[RS * 4 + 2 * lane];
+      new_v[0] = nv.x;
+      new_v[1] = nv.y;
+    }
+    fold_in(new_st, new_v[0], new_v[1]);
+  }
   __syncthreads();
   finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
   KVQ_STAMP(11);
@@ -1695,16 +1742,16 @@ static int64_t workspace_bytes_for(const Plan& p, int64_t D) {
   return ws_cnt_bytes(p) + ws_ml_bytes(p) + (int64_t)p.n_units * p.n_split * p.rows * D * 4;
 }
 
-// Waves per workgroup of the MFMA kernel: one row set runs 8 waves (two per
-// SIMD hide each other's latency); two row sets need more registers than that
-// allows and run 4. Tiles whose loads a wave keeps in flight: one with one row
-// set (its SIMD partner covers the latency; a second slot measured 5-12 %
-// slower from 4K to 128K keys), two with two row sets (one wave per SIMD;
-// one slot measured 8 % slower).
+// Waves per workgroup of the MFMA kernel: 8 (two per SIMD hide each other's
+// latency), with one tile's loads in flight per wave (the SIMD partner covers
+// the latency; a second slot measured 5-12 % slower from 4K to 128K keys with
+// one row set). Two row sets fit two waves per SIMD too (212-223 VGPRs, no
+// AGPRs) once the MFMA accumulators stay in VGPRs and the loop-invariant
+// values live in LDS; before that they ran 4 waves with two tiles in flight.
 template <int RS>
-constexpr int mfma_waves() { return RS == 1 ? 8 : 4; }
+constexpr int mfma_waves() { return 8; }
 template <int RS>
-constexpr int mfma_tiles_in_flight() { return RS == 1 ? 1 : 2; }
+constexpr int mfma_tiles_in_flight() { return 1; }
 
 template <int D, int RS, int QM, int SM, bool PAGED>
 static void launch_mfma_rs(const AttnArgs& a, bool rowmask, dim3 grid, hipStream_t st) {

@@ -21,6 +21,11 @@ CSRC = os.path.join(PKG_ROOT, "csrc")
 OUT = os.path.join(_HERE, "libkvint4.so")
 
 SOURCES = ("kvq_capi.hip", "kvq_quant.hip", "kvq_attn.hip", "kvq_prefill.hip")
+# Per-source flags. The decode kernels keep their MFMA accumulators in VGPRs:
+# the compiler's default puts the PV accumulators in AGPRs, and the two-row-set
+# kernel then copies about 72 values between AGPRs and VGPRs on every tile
+# (its VALU uses them, for the lazy rescale), with ~100 registers held twice.
+SOURCE_FLAGS = {"kvq_attn.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=true")}
 ARCH = os.environ.get("KVQ_OFFLOAD_ARCH", "gfx950")
 
 # Packed-FP32 VALU forms are kept out of the generated code (the value path is
@@ -46,7 +51,9 @@ def hipcc() -> str:
 # The measurement library behind bench.py --stream-probe: the streaming-read
 # probe kernels and the decode kernels built with phase stamps.
 PROBE_OUT = os.path.join(_HERE, "libkvq_probe.so")
-PROBE_SOURCES = (("probe/kvq_probe.hip", ()), ("kvq_attn.hip", ("-DKVQ_PHASE_STAMPS=1",)), ("kvq_capi.hip", ()))
+PROBE_SOURCES = (("probe/kvq_probe.hip", ()),
+                 ("kvq_attn.hip", SOURCE_FLAGS["kvq_attn.hip"] + ("-DKVQ_PHASE_STAMPS=1",)),
+                 ("kvq_capi.hip", ()))
 
 
 def _build_libs(libs, verbose: bool) -> None:
@@ -90,5 +97,6 @@ def _build_libs(libs, verbose: bool) -> None:
 def build(verbose: bool = False) -> str:
     """Compile every HIP source into kvint4/libkvint4.so (the product) and
     kvint4/libkvq_probe.so (measurement only); return the product's path."""
-    _build_libs([(OUT, [(s, ()) for s in SOURCES]), (PROBE_OUT, list(PROBE_SOURCES))], verbose)
+    _build_libs([(OUT, [(s, SOURCE_FLAGS.get(s, ())) for s in SOURCES]), (PROBE_OUT, list(PROBE_SOURCES))],
+                verbose)
     return OUT
