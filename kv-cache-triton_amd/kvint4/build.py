@@ -25,7 +25,10 @@ SOURCES = ("kvq_capi.hip", "kvq_quant.hip", "kvq_attn.hip", "kvq_prefill.hip")
 # the compiler's default puts the PV accumulators in AGPRs, and the two-row-set
 # kernel then copies about 72 values between AGPRs and VGPRs on every tile
 # (its VALU uses them, for the lazy rescale), with ~100 registers held twice.
-SOURCE_FLAGS = {"kvq_attn.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=true")}
+# The prefill kernel's one-row-block variant likewise drops its 32 AGPRs
+# (176 copies) and runs four waves per SIMD instead of three.
+SOURCE_FLAGS = {"kvq_attn.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=true"),
+                "kvq_prefill.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=true")}
 ARCH = os.environ.get("KVQ_OFFLOAD_ARCH", "gfx950")
 
 # Packed-FP32 VALU forms are kept out of the generated code (the value path is
