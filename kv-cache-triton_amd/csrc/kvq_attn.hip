@@ -684,12 +684,13 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // With two row sets, values the tile loop does not change are kept in LDS
   // rather than registers, so that the kernel fits two waves per SIMD: each
   // wave's accumulator init per (row set, chunk), the same in every lane;
-  // and the decode step's new token (its scores per row, then two
-  // dequantized value elements per lane), folded in after the loop. One row
-  // set has registers to spare and keeps them in registers.
+  // and the decode step's new-token scores, folded in after the loop. One
+  // row set has registers to spare and keeps them in registers.
   constexpr bool KEEP_IN_LDS = RS > 1;
   __shared__ __attribute__((aligned(16))) float qb_lds[KEEP_IN_LDS ? NW : 1][RS][LPT][4];
-  __shared__ __attribute__((aligned(16))) float nt_lds[KEEP_IN_LDS ? RS * 4 + 128 : 1];
+  // the decode step's new token: its scores per row (two row sets only),
+  // then two dequantized value elements per lane
+  __shared__ __attribute__((aligned(16))) float nt_lds[RS * 4 + 128];
   auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem);
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
@@ -740,6 +741,29 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // attended by the unit's last split from registers
   bool has_new = a.append && L < a.Sk && split == a.n_split - 1;
   L = L < a.Sk ? L : a.Sk;
+  // The new token's rows (lane l: elements 2l, 2l+1): the K row for the
+  // split's last wave, which quantizes, stores and scores it, the V row for
+  // the wave before it, which quantizes and stores it and leaves its
+  // dequantized values in LDS (two waves share the work that one wave of
+  // the split has on top of its tile). Loaded before the cache tiles where
+  // registers allow: loads complete in issue order, so loaded after them a
+  // row is waited for only once the whole tile has arrived, and the
+  // new-token work starts late instead of overlapping the tile's transfer.
+  // The kernel that runs four waves per SIMD has no register to spare over
+  // that stretch (holding the row there spills) and loads it after the
+  // tile. (A paged cache may still find no block for the row; it is then
+  // loaded and left unused.)
+  constexpr bool EARLY_NEW = mfma_waves_per_simd<D, RS>() < 4;
+  uint32_t new_x2 = 0u;
+  auto load_new_row = [&]() {
+    if (has_new && wave >= NW - 2 && lane < D / 2) {
+      const bool is_k = wave == NW - 1;  // wave-uniform
+      const uint16_t* xrow = is_k ? (const uint16_t*)a.knew + (int64_t)b * a.kns_b + (int64_t)kvh * a.kns_h
+                                  : (const uint16_t*)a.vnew + (int64_t)b * a.vns_b + (int64_t)kvh * a.vns_h;
+      new_x2 = *((const uint32_t*)xrow + lane);
+    }
+  };
+  if constexpr (EARLY_NEW) load_new_row();
   int t_begin, t_end;
   if constexpr (PAGED) split_range64(a, L, split, t_begin, t_end);
   else split_range(a, L, split, t_begin, t_end);
@@ -927,14 +951,11 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
     tail_ks = __builtin_amdgcn_raw_buffer_load_b16(rks, tt * kss2 + sg, 0, 0);
     tail_vs = __builtin_amdgcn_raw_buffer_load_b16(rvs, tt * vss2 + sg, 0, 0);
   }
-  // decode step: the last wave of the unit's last split holds the new
-  // token's K and V elements 2l, 2l+1 (lane l)
-  uint32_t new_k2 = 0u, new_v2 = 0u;
-  const bool new_here = has_new && wave == NW - 1;
-  if (new_here && lane < D / 2) {
-    new_k2 = *((const uint32_t*)((const uint16_t*)a.knew + (int64_t)b * a.kns_b + (int64_t)kvh * a.kns_h) + lane);
-    new_v2 = *((const uint32_t*)((const uint16_t*)a.vnew + (int64_t)b * a.vns_b + (int64_t)kvh * a.vns_h) + lane);
-  }
+  if constexpr (!EARLY_NEW) load_new_row();
+  // decode step: the split's last wave takes the new token's K row, the
+  // wave before it the V row
+  const bool new_k_here = has_new && wave == NW - 1;
+  const bool new_v_here = has_new && wave == NW - 2;
   // query rows -> this wave's LDS copy, permuted to the key operand order:
   // (e0,e2) (e1,e3) (e4,e6) (e5,e7) of every 8 elements
 #pragma unroll
@@ -1043,61 +1064,59 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       }
     }
   };
-  // decode step: quantize the new K and V rows exactly as the quantize kernel
+  // decode step: quantize the new K or V row exactly as the quantize kernel
   // does (group absmax / 7 in fp32, IEEE division, round half to even, clamp,
-  // +8; scale narrowed once for storage), store them at row L, and score the
-  // dequantized key (stored scale) now, while the tiles are in flight; the
-  // fold happens after the loop. Lane l owns code byte l of the packed row
+  // +8; scale narrowed once for storage) and store it at row L, while the
+  // tiles are in flight. The K wave scores the dequantized key (stored
+  // scale) now; the V wave leaves the dequantized values in LDS; the K wave
+  // folds both in after the loop. Lane l owns code byte l of the packed row
   // (packed width = groups x G/2 bytes <= 64).
   float new_st[RS][4];
-  float new_v[2] = {0.0f, 0.0f};
-  if (new_here) {
+  if (new_k_here || new_v_here) {  // wave-uniform
+    const bool is_k = new_k_here;
     const int G = a.G;
     const int W = ((D + G - 1) / G) * (G / 2);
     const bool byte_ok = lane < W;
-    float deq[2][2];
-#pragma unroll
-    for (int kvsel = 0; kvsel < 2; ++kvsel) {
-      const uint32_t x2 = kvsel == 0 ? new_k2 : new_v2;
-      const float x0 = col_ok ? (F16 ? f16_bits_to_f32(x2 & 0xffffu) : bf16_bits_to_f32(x2 & 0xffffu)) : 0.0f;
-      const float x1 = col_ok ? (F16 ? f16_bits_to_f32(x2 >> 16) : bf16_bits_to_f32(x2 >> 16)) : 0.0f;
-      // group absmax: G / 2 consecutive lanes (16, 32 or 64)
-      float am = row16_max(fmax_nc(fabsf(x0), fabsf(x1)));
-      if (G >= 64) {  // rows of 16 lanes pairwise: (0, 1), (2, 3)
-        float u = am, v = am;
-        permlane16_swap(u, v);
-        am = fmax_nc(u, v);
-      }
-      if (G >= 128) {  // halves of 32 lanes
-        float u = am, v = am;
-        permlane32_swap(u, v);
-        am = fmax_nc(u, v);
-      }
-      const float scale = am > 0.0f ? am / 7.0f : 1.0f;
-      float c0 = __builtin_rintf(x0 / scale), c1 = __builtin_rintf(x1 / scale);
-      c0 = fminf(fmaxf(c0, -8.0f), 7.0f);
-      c1 = fminf(fmaxf(c1, -8.0f), 7.0f);
-      const uint32_t byte = (uint32_t)((int)c0 + 8) | ((uint32_t)((int)c1 + 8) << 4);
-      const uint32_t sbits = S_F16 ? f32_to_f16_bits(scale) : f32_to_bf16_bits(scale);
-      uint8_t* prow = const_cast<uint8_t*>(kvsel == 0 ? kp_bh : vp_bh) + new_row * (kvsel == 0 ? kps : vps);
-      uint16_t* srow = const_cast<uint16_t*>(kvsel == 0 ? ks_bh : vs_bh) + new_row * (kvsel == 0 ? a.kss_s : a.vss_s);
-      if (byte_ok) prow[lane] = (uint8_t)byte;
-      if (byte_ok && (2 * lane) % G == 0) srow[(2 * lane) / G] = (uint16_t)sbits;
-      const float sq = scale16_to_f32(sbits, S_F16);
-      deq[kvsel][0] = c0 * sq;
-      deq[kvsel][1] = c1 * sq;
+    const float x0 = col_ok ? (F16 ? f16_bits_to_f32(new_x2 & 0xffffu) : bf16_bits_to_f32(new_x2 & 0xffffu)) : 0.0f;
+    const float x1 = col_ok ? (F16 ? f16_bits_to_f32(new_x2 >> 16) : bf16_bits_to_f32(new_x2 >> 16)) : 0.0f;
+    // group absmax: G / 2 consecutive lanes (16, 32 or 64)
+    float am = row16_max(fmax_nc(fabsf(x0), fabsf(x1)));
+    if (G >= 64) {  // rows of 16 lanes pairwise: (0, 1), (2, 3)
+      float u = am, v = am;
+      permlane16_swap(u, v);
+      am = fmax_nc(u, v);
     }
-    key_scores(deq[0][0], deq[0][1], L, new_st);
-    new_v[0] = deq[1][0];
-    new_v[1] = deq[1][1];
-    if constexpr (KEEP_IN_LDS) {
-      if (lane == 0) {
+    if (G >= 128) {  // halves of 32 lanes
+      float u = am, v = am;
+      permlane32_swap(u, v);
+      am = fmax_nc(u, v);
+    }
+    const float scale = am > 0.0f ? am / 7.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
+    float c0 = rint_quotient(x0, scale, inv, fast), c1 = rint_quotient(x1, scale, inv, fast);
+    c0 = fminf(fmaxf(c0, -8.0f), 7.0f);
+    c1 = fminf(fmaxf(c1, -8.0f), 7.0f);
+    const uint32_t byte = (uint32_t)((int)c0 + 8) | ((uint32_t)((int)c1 + 8) << 4);
+    const uint32_t sbits = S_F16 ? f32_to_f16_bits(scale) : f32_to_bf16_bits(scale);
+    uint8_t* prow = const_cast<uint8_t*>(is_k ? kp_bh : vp_bh) + new_row * (is_k ? kps : vps);
+    uint16_t* srow = const_cast<uint16_t*>(is_k ? ks_bh : vs_bh) + new_row * (is_k ? a.kss_s : a.vss_s);
+    if (byte_ok) prow[lane] = (uint8_t)byte;
+    if (byte_ok && (2 * lane) % G == 0) srow[(2 * lane) / G] = (uint16_t)sbits;
+    const float sq = scale16_to_f32(sbits, S_F16);
+    const float d0 = c0 * sq, d1 = c1 * sq;
+    if (is_k) {
+      key_scores(d0, d1, L, new_st);
+      if constexpr (KEEP_IN_LDS) {
+        if (lane == 0) {
 #pragma unroll
-        for (int rs = 0; rs < RS; ++rs)
+          for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) nt_lds[rs * 4 + r] = new_st[rs][r];
+            for (int r = 0; r < 4; ++r) nt_lds[rs * 4 + r] = new_st[rs][r];
+        }
       }
-      *(float2*)&nt_lds[RS * 4 + 2 * lane] = make_float2(new_v[0], new_v[1]);
+    } else {
+      *(float2*)&nt_lds[RS * 4 + 2 * lane] = make_float2(d0, d1);
     }
   }
 
@@ -1347,6 +1366,11 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // ---- extra keys folded into this wave's partial (already in LDS): the
   //      split's tail key of this wave and, in a decode step, the new token
   //      (scored before the tile loop). ----
+  // The tail key's raw loads are touched only here: an empty asm that
+  // redefines them keeps the compiler from converting them right after the
+  // loads, which (loads completing in issue order) would wait for the whole
+  // tile before the loop.
+  asm volatile("" : "+v"(tail_kb), "+v"(tail_vb), "+v"(tail_ks), "+v"(tail_vs)::"memory");
   if (wave < n_tail) {
     const float ksf = scale16_to_f32(tail_ks, S_F16), vsf = scale16_to_f32(tail_vs, S_F16);
     float st[RS][4];
@@ -1354,20 +1378,17 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
                tail_t, st);
     fold_in(st, ((float)(int)(tail_vb & 15u) - 8.0f) * vsf, ((float)(int)((tail_vb >> 4) & 15u) - 8.0f) * vsf);
   }
-  if (new_here) {
+  if (new_k_here) {
+    // the V wave wrote its values before its tile loop, so before the
+    // workgroup barrier above
     if constexpr (KEEP_IN_LDS) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
         for (int r = 0; r < 4; ++r) new_st[rs][r] = nt_lds[rs * 4 + r];
-      const float2 nv = *(const float2*)&nt_lds[RS * 4 + 2 * lane];
-      new_v[0] = nv.x;
-      new_v[1] = nv.y;
     }
-    fold_in(new_st, new_v[0], new_v[1]);
+    const float2 nv = *(const float2*)&nt_lds[RS * 4 + 2 * lane];
+    fold_in(new_st, nv.x, nv.y);
   }
   __syncthreads();
   finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);

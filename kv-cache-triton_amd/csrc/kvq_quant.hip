@@ -109,20 +109,6 @@ __device__ __forceinline__ float dpp_f(float v) {
                                                                0xF, 0xF, false));
 }
 
-// rint(x / s) where x / s is the IEEE (correctly rounded) fp32 quotient, for
-// |x| <= 7 s (x an element of the group whose absmax / 7 is s, s normal):
-// t = x * (1 / s), both steps correctly rounded, lies within 2^-19.6 of the
-// rounded quotient (relative error 2^-23 on |x / s| <= 7, plus the quotient's
-// own rounding of 2^-21), so rint(t) is rint of the quotient unless t is
-// within that distance of a half-integer; those rare elements (and groups
-// whose scale is not a moderate normal number) take the division itself. The
-// threshold used, 2^-17, leaves a margin of 6x.
-__device__ __forceinline__ float rint_quotient(float x, float s, float inv, bool fast) {
-  const float t = x * inv;
-  const float r = __builtin_rintf(t);
-  if (fast && !(fabsf(t - r) > 0.5f - 0x1p-17f)) return r;
-  return __builtin_rintf(x / s);
-}
 
 // Each thread takes chunk ch of RPT rows (row slot r0 and r0 + k * rq); for
 // every k the G/8 lanes of a group hold adjacent chunks of one row. All of
