@@ -506,10 +506,16 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
 // the merger's loads are issued only after its own atomic returned the final
 // count, and they miss its L1 and read the L2 the stores completed in. (One
 // counter per unit: a two-level count measured 0.3 us slower.)
+//
+// nt (may be null): one more partial, a single key, folded in with the
+// waves' ones: its score per row at nt[r] (max = score, sum = 1; kNeg for a
+// row it is masked from) and its values at nt[ROWS + d], the same for every
+// row. The MFMA kernel's decode step passes the new token this way.
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int split, int rc,
                                              int kvh, int b, const float (*o_lds)[ROWS][D],
-                                             const float (*ml_lds)[ROWS][2], MergeLds<64 * NW>& mg) {
+                                             const float (*ml_lds)[ROWS][2], MergeLds<64 * NW>& mg,
+                                             const float* nt = nullptr) {
   constexpr int NT = 64 * NW;
   const int tid = threadIdx.x;
   const bool single = a.n_split == 1;
@@ -524,12 +530,19 @@ __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int sp
       lw[w] = ml.y;
       M = fmax_nc(M, ml.x);
     }
+    const float sn = nt != nullptr ? nt[r] : kNeg;
+    M = fmax_nc(M, sn);
     float Ls = 0.0f, Os = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float f = __builtin_amdgcn_exp2f(mw[w] - M);
       Ls = fmaf(lw[w], f, Ls);
       Os = fmaf(o_lds[w][r][d], f, Os);
+    }
+    if (nt != nullptr) {  // workgroup-uniform
+      const float f = sn > kNeg ? __builtin_amdgcn_exp2f(sn - M) : 0.0f;
+      Ls += f;
+      Os = fmaf(nt[ROWS + d], f, Os);
     }
     const int rho = rc * ROWS + r;
     if (single) {
@@ -681,15 +694,14 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
   __shared__ __attribute__((aligned(16))) float ml_lds[NW][ROWS][2];
   __shared__ MergeLds<64 * NW> mg;
-  // With two row sets, values the tile loop does not change are kept in LDS
-  // rather than registers, so that the kernel fits two waves per SIMD: each
-  // wave's accumulator init per (row set, chunk), the same in every lane;
-  // and the decode step's new-token scores, folded in after the loop. One
-  // row set has registers to spare and keeps them in registers.
+  // With two row sets, each wave's accumulator init per (row set, chunk),
+  // the same in every lane and unchanged by the tile loop, is kept in LDS
+  // rather than registers, so that the kernel fits two waves per SIMD. One
+  // row set has registers to spare and keeps it in registers.
   constexpr bool KEEP_IN_LDS = RS > 1;
   __shared__ __attribute__((aligned(16))) float qb_lds[KEEP_IN_LDS ? NW : 1][RS][LPT][4];
-  // the decode step's new token: its scores per row (two row sets only),
-  // then two dequantized value elements per lane
+  // the decode step's new token: its score per row, then its dequantized
+  // values (two elements per lane of the V wave)
   __shared__ __attribute__((aligned(16))) float nt_lds[RS * 4 + 128];
   auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem);
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
@@ -1068,10 +1080,10 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // does (group absmax / 7 in fp32, IEEE division, round half to even, clamp,
   // +8; scale narrowed once for storage) and store it at row L, while the
   // tiles are in flight. The K wave scores the dequantized key (stored
-  // scale) now; the V wave leaves the dequantized values in LDS; the K wave
-  // folds both in after the loop. Lane l owns code byte l of the packed row
-  // (packed width = groups x G/2 bytes <= 64).
-  float new_st[RS][4];
+  // scale) now and leaves the scores in LDS, the V wave the dequantized
+  // values; the workgroup fold takes them in as one more partial. Lane l
+  // owns code byte l of the packed row (packed width = groups x G/2 bytes
+  // <= 64).
   if (new_k_here || new_v_here) {  // wave-uniform
     const bool is_k = new_k_here;
     const int G = a.G;
@@ -1106,14 +1118,13 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
     const float sq = scale16_to_f32(sbits, S_F16);
     const float d0 = c0 * sq, d1 = c1 * sq;
     if (is_k) {
+      float new_st[RS][4];
       key_scores(d0, d1, L, new_st);
-      if constexpr (KEEP_IN_LDS) {
-        if (lane == 0) {
+      if (lane == 0) {
 #pragma unroll
-          for (int rs = 0; rs < RS; ++rs)
+        for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) nt_lds[rs * 4 + r] = new_st[rs][r];
-        }
+          for (int r = 0; r < 4; ++r) nt_lds[rs * 4 + r] = new_st[rs][r];
       }
     } else {
       *(float2*)&nt_lds[RS * 4 + 2 * lane] = make_float2(d0, d1);
@@ -1378,20 +1389,10 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
                tail_t, st);
     fold_in(st, ((float)(int)(tail_vb & 15u) - 8.0f) * vsf, ((float)(int)((tail_vb >> 4) & 15u) - 8.0f) * vsf);
   }
-  if (new_k_here) {
-    // the V wave wrote its values before its tile loop, so before the
-    // workgroup barrier above
-    if constexpr (KEEP_IN_LDS) {
-#pragma unroll
-      for (int rs = 0; rs < RS; ++rs)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) new_st[rs][r] = nt_lds[rs * 4 + r];
-    }
-    const float2 nv = *(const float2*)&nt_lds[RS * 4 + 2 * lane];
-    fold_in(new_st, nv.x, nv.y);
-  }
   __syncthreads();
-  finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
+  // the new token (scores and values in LDS, written by the K and V waves
+  // before their tile loops) joins the waves' partials in the workgroup fold
+  finish_block<ROWS, D, QM, NW>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg, has_new ? nt_lds : nullptr);
   KVQ_STAMP(11);
 }
 
