@@ -108,6 +108,15 @@ def main() -> int:
                          "WRITE_SIZE run of this script with --calib-copy-mib) into a traffic summary on stdout")
     ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
                     help="no GPU work: turn a rocprofv3 --kernel-trace --stats kernel_stats.csv into a summary")
+    ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
+                    help="no GPU work: per-dispatch, per-wave and per-tile medians of the decode kernel's "
+                         "counters in a rocprofv3 --pmc counter_collection.csv")
+    ap.add_argument("--tiles-per-wave", type=float, default=1.0,
+                    help="64-key tiles each wave of the profiled decode kernel takes (for --summarize-counters)")
+    ap.add_argument("--note", default="", help="description line recorded in a counter summary")
+    ap.add_argument("--summarize-probe", metavar="PROBE_JSON",
+                    help="no GPU work: format the JSON line of a --stream-probe run (ceiling per grid, issue "
+                         "cost, decode-step time and phases) as text")
     ap.add_argument("--cmd", default="", help="command line recorded in a summary")
     args = ap.parse_args()
 
@@ -116,6 +125,12 @@ def main() -> int:
         return 0
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.cmd))
+        return 0
+    if args.summarize_probe:
+        print(summarize_probe(args.summarize_probe))
+        return 0
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.tiles_per_wave, args.note, args.cmd))
         return 0
 
     if args.gpus != 1:
@@ -863,6 +878,77 @@ def summarize_pmc(fetch_csv: str, write_csv: str, calib_mib: int, cmd: str) -> s
     out.append(f"fetch_bytes_per_launch: {res['FETCH_SIZE'] * 1024.0:.0f}")
     out.append(f"write_bytes_per_launch: {res['WRITE_SIZE'] * 1024.0:.0f}")
     return "\n".join([f"command: {cmd}" if cmd else "command: (not recorded)"] + out)
+
+
+def summarize_counters(path: str, tiles_per_wave: float, note: str, cmd: str) -> str:
+    """Counter summary of the decode kernel (the decode_attn_ kernel with the
+    most dispatches): for each counter its median per dispatch, that divided by
+    the dispatch's waves (Grid_Size / 64), and by tiles_per_wave; plus VALU
+    issue = SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES when both were collected."""
+    import csv
+    import statistics
+
+    vals: dict = {}
+    grids: dict = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"]
+            if "decode_attn_" not in name:
+                continue
+            vals.setdefault(name, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+            grids.setdefault(name, []).append(int(row["Grid_Size"]))
+    if not vals:
+        raise SystemExit("no decode_attn_ kernel in the counter input")
+    name = max(vals, key=lambda n: len(grids[n]))
+    waves = statistics.median(grids[name]) / 64.0
+    out = [f"command: {cmd}" if cmd else "command: (not recorded)", f"kernel: {name[:110]}"]
+    if note:
+        out.append(note)
+    out.append(f"{'counter':<22} {'median/dispatch':>16} {'per wave':>10} {'per tile':>10}  (dispatches)")
+    med = {}
+    for c in sorted(vals[name]):
+        m = statistics.median(vals[name][c])
+        med[c] = m
+        out.append(f"{c:<22} {m:16.0f} {m / waves:10.1f} {m / waves / tiles_per_wave:10.1f}  "
+                   f"({len(vals[name][c])})")
+    if "SQ_ACTIVE_INST_VALU" in med and med.get("SQ_WAVE_CYCLES"):
+        out.append(f"VALU issue fraction SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES = "
+                   f"{med['SQ_ACTIVE_INST_VALU'] / med['SQ_WAVE_CYCLES']:.3f}")
+    return "\n".join(out)
+
+
+def summarize_probe(path: str) -> str:
+    """Text form of a --stream-probe JSON line (its last line in `path`)."""
+    d = json.loads(open(path).read().strip().splitlines()[-1])
+    best = d["best"]
+    out = [f"streaming read of {d['bytes_per_launch']} B per launch, {d['layers']} buffers, graph of "
+           f"{d['layers']} launches x 20 replays:"]
+    for r in d["stream"]:
+        out.append(f"  grid {r['grid']:5d} x {r['block']:4d}  {r['pieces_per_thread']:2d} x 16 B per thread  "
+                   f"{r['us_per_launch']:7.3f} us/launch  {r['gbs']:7.1f} GB/s")
+    for r in d.get("issue_cost", []):
+        out.append(f"  grid   256 x  512  10 x 16 B per thread with {r['valu_instructions']:4d} VALU "
+                   f"{r['placed']:<12}  {r['us_per_launch']:7.3f} us/launch")
+    dec = d["decode_step"]
+    out.append(f"decode step (product kernel, same graph timing): {dec['us_per_launch']:.3f} us/launch = "
+               f"{dec['gbs']:.1f} GB/s, {dec['frac_of_best_read']:.3f} of the best read "
+               f"({best['us_per_launch']:.3f} us)")
+
+    def table(title, phases, keys):
+        rows = [f"{title:<60}{'min':>6}{'med':>8}{'p90':>8}{'max':>8}"]
+        for k in keys:
+            if k in phases:
+                v = phases[k]
+                label = f"  {k:<22} (n {v['n']:4d})" if "n" in v else f"  {k:<22}"
+                rows.append(f"{label:<60}{v['min']:6.0f}{v['med']:8.0f}{v['p90']:8.0f}{v['max']:8.0f}")
+        return rows
+
+    sp = d["stream_phases_ns"]
+    out += table(f"streaming read, per-wave stamps (grid {sp['grid']} x {sp['block']}), ns:", sp,
+                 ("entry", "loads_issued", "first_arrived", "all_arrived"))
+    out += table("decode step, instrumented build (libkvq_probe.so), per wave, ns:", d["decode_phases_ns"],
+                 list(d["decode_phases_ns"]))
+    return "\n".join(out)
 
 
 def summarize_trace(stats_csv: str, cmd: str) -> str:
