@@ -334,12 +334,21 @@ __device__ __forceinline__ void split_range64(const AttnArgs& a, int L, int spli
   t1 = split + 1 == ns ? L : (div_splits(a, (uint32_t)(split + 1) * (uint32_t)L) & ~63);
 }
 
+// Block-table entry of page pg of a sequence (bt_b = its table row), -1 past
+// the row's last column. pg must be wave-uniform: the entry is read through
+// the scalar cache (no kernel of the launch writes the table), so waiting for
+// it does not wait for vector loads issued before it (the query rows).
+__device__ __forceinline__ int32_t table_entry(const AttnArgs& a, const int32_t* bt_b, uint32_t pg) {
+  return pg < (uint32_t)a.bt_cols ? load_const_i32(bt_b, (int)pg) : -1;
+}
+
 // Pool row offset of token t of a paged sequence (bt_b = its block table
 // row), relative to t: row = t + delta. ok is false when no block holds t.
+// t must be wave-uniform.
 __device__ __forceinline__ void page_delta(const AttnArgs& a, const int32_t* bt_b, uint32_t t,
                                            uint32_t& delta, bool& ok) {
   const uint32_t pg = t >> a.page_shift;
-  const int32_t blk = pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1;
+  const int32_t blk = table_entry(a, bt_b, pg);
   ok = blk >= 0 && blk < a.n_blocks;
   delta = ((uint32_t)blk - pg) << a.page_shift;
 }
@@ -711,6 +720,9 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   KVQ_STAMP(0);
   fetch_prologue_args(a);
+  // paged: one field of the block table's argument line in the first batch,
+  // so that the line is in the scalar cache when the table is read
+  if constexpr (PAGED) asm volatile("" ::"s"(a.bt_cols));
   int unit, split;
   if (!unit_and_split(a, unit, split)) return;
   int b, kvh, rc;
@@ -846,7 +858,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       const uint32_t k = (((t0 - (uint32_t)t_begin) >> 6) - (uint32_t)wave) / (uint32_t)NW;  // wave-uniform
       int32_t blk;
       if (k >= (uint32_t)CH && k < 64u) blk = __builtin_amdgcn_readlane(wave_blk, (int)k);
-      else blk = __builtin_amdgcn_readfirstlane(pg < (uint32_t)a.bt_cols ? bt_b[pg] : -1);
+      else blk = table_entry(a, bt_b, pg);
       const bool ok = blk >= 0 && blk < a.n_blocks && t0 < (uint32_t)t_end;
       // wave-uniform; readfirstlane keeps the tile's buffers in scalar registers
       rb = __builtin_amdgcn_readfirstlane(ok ? t0 + (((uint32_t)blk - pg) << a.page_shift) : 0u);
