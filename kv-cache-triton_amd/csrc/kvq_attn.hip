@@ -720,9 +720,13 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   KVQ_STAMP(0);
   fetch_prologue_args(a);
-  // paged: one field of the block table's argument line in the first batch,
-  // so that the line is in the scalar cache when the table is read
-  if constexpr (PAGED) asm volatile("" ::"s"(a.bt_cols));
+  // One field of each of the argument block's last two 64-byte lines in the
+  // first batch as well, so that both lines are in the scalar cache before
+  // anything else reads them: the block table (paged kernels) before the first
+  // tile, and the workspace pointers, whose load the compiler places among
+  // the query's LDS reads (a scalar load in flight turns those reads' waits
+  // into waits for it too).
+  asm volatile("" ::"s"(a.bt_cols), "s"(a.ws_o));
   int unit, split;
   if (!unit_and_split(a, unit, split)) return;
   int b, kvh, rc;
