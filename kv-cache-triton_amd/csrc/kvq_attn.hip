@@ -1003,6 +1003,21 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int my_row = lane & 3;
+  // The one-row-set kernel for D = 128 has registers to spare (two waves per
+  // SIMD, 256 VGPRs each): it keeps this lane's query operands (its row's 16
+  // dwords of 4 packed elements) in registers across the tile loop instead
+  // of reading them from LDS before each matrix instruction, where the
+  // compiler waits for each read alone.
+  constexpr bool Q_IN_REGS = RS == 1 && D == 128;
+  u32x4_t qreg[Q_IN_REGS ? 4 * LPT : 1];
+  if constexpr (Q_IN_REGS) {
+#pragma unroll
+    for (int kd = 0; kd < 4 * LPT; ++kd) qreg[kd] = *(const u32x4_t*)&q_lds[wave][my_row][4 * kd];
+  }
+  auto q_operand = [&](int rs, int kd) -> u32x4_t {
+    if constexpr (Q_IN_REGS) return qreg[kd];
+    else return *(const u32x4_t*)&q_lds[wave][rs * 4 + my_row][4 * kd];
+  };
   // accumulator init -bias * sum(q) per 32-dim chunk, on the MFMA (every
   // lane gets the same four row values; with two row sets lane 0 keeps them
   // in LDS)
@@ -1014,7 +1029,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) {
-        const u32x4_t q4 = *(const u32x4_t*)&q_lds[wave][rs * 4 + my_row][16 * c + 4 * k4];
+        const u32x4_t q4 = q_operand(rs, 4 * c + k4);
         acc = mfma4<F16>(q4.x, q4.y, NEG_BIAS, NEG_BIAS, acc);
         acc = mfma4<F16>(q4.z, q4.w, NEG_BIAS, NEG_BIAS, acc);
       }
@@ -1195,7 +1210,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
             const uint32_t b57 = __builtin_amdgcn_perm(MAGIC, hi, SEL_46);  // (e5, e7)
 #pragma unroll
             for (int rs = 0; rs < RS; ++rs) {
-              const u32x4_t q4 = *(const u32x4_t*)&q_lds[wave][rs * 4 + my_row][4 * kd];
+              const u32x4_t q4 = q_operand(rs, kd);
               acc[rs][c] = mfma4<F16>(q4.x, q4.y, b02, b13, acc[rs][c]);
               acc[rs][c] = mfma4<F16>(q4.z, q4.w, b46, b57, acc[rs][c]);
             }
