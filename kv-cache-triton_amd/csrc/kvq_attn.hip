@@ -1734,13 +1734,14 @@ static bool use_mfma(int q_dtype, int scale_dtype) {
 }
 
 // Fewest keys a split is given (when the sequence is long enough to split):
-// two 64-token MFMA tiles, or four 16/32-token VALU tiles.
-// Shortest split worth its share of the cross-split merge (measured): the
-// matrix-core kernel runs a 64-key tile per wave in well under the merge's
-// cost, the exact-fp32 VALU kernel needs about 1024 keys per split.
+// the shortest split worth its share of the cross-split merge (measured):
+// two 64-token tiles for the matrix-core kernel; the same 128 keys for the
+// exact-fp32 VALU kernel (GPT-2-small shape, 1K keys, 12 heads: one split
+// per head 11.8 us, 2 splits 10.6, 4 splits 9.1, 8 splits 8.3, 16 splits 8.4).
 static int64_t min_split_tokens(bool mfma, int64_t D) {
+  (void)mfma;
   (void)D;
-  return mfma ? 128 : 1024;
+  return 128;
 }
 
 // Split-K plan: enough splits that B * Hkv * row_chunks * n_split workgroups

@@ -47,9 +47,10 @@ def test_num_splits_planning():
     assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 128, 100, B16, B16, 256) == 1
     # plenty of units already -> one split
     assert lib.kvq_decode_attn_num_splits(16, 25, 25, 1, 64, 1024, F16, F16, 256) == 1
-    # fp32 queries plan for the VALU kernel: no split shorter than 1024 keys
-    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 1024, F32, F16, 256) == 1
-    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 16384, F32, F16, 256) == 16
+    # fp32 queries plan for the VALU kernel the same way: no split shorter than
+    # 128 keys (1K keys: 8 splits), otherwise enough splits to cover the CUs
+    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 1024, F32, F16, 256) == 8
+    assert lib.kvq_decode_attn_num_splits(1, 12, 12, 1, 64, 16384, F32, F16, 256) == 22
     assert lib.kvq_decode_attn_num_splits(1, 32, 8, 1, 96, 1024, B16, B16, 256) == nat.KVQ_EUNSUP
     assert lib.kvq_decode_attn_num_splits(1, 30, 8, 1, 128, 1024, B16, B16, 256) == nat.KVQ_EINVAL
     # an empty batch or query block launches nothing: one split, no workspace
