@@ -176,10 +176,11 @@ def main() -> int:
     seq_plus = (seq_lens + 1) if seq_lens is not None else None
 
     # The fused decode step (one launch per layer: the new token's K/V are
-    # quantized into the cache and attended along with it) needs 16-bit
-    # activations and group size 32/64/128; otherwise, or with --unfused, a
-    # layer takes three launches (quantize K, quantize V, attention).
-    fused = not args.unfused and w["dtype"] != "f32" and G in (32, 64, 128)
+    # quantized into the cache and attended along with it) takes group size
+    # 32/64/128, and a paged cache 16-bit activations; otherwise, or with
+    # --unfused, a layer takes three launches (quantize K, quantize V,
+    # attention).
+    fused = not args.unfused and G in (32, 64, 128) and not (P and w["dtype"] == "f32")
 
     def attn(layer):
         if P:
@@ -333,8 +334,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(args.traffic_summary, w),
-            "kernel": ("decode_attn_mfma_kernel (decode step: append + attention)" if fused else
-                       "decode_attn_mfma_kernel" if w["dtype"] != "f32" else "decode_attn_valu_kernel"),
+            "kernel": ("decode_attn_mfma_kernel" if w["dtype"] != "f32" else "decode_attn_valu_kernel")
+                      + (" (decode step: append + attention)" if fused else ""),
             "bytes_per_launch": k_bytes,
         },
     }

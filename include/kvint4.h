@@ -167,12 +167,14 @@ int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_strides,
  * kvq_quantize's and the attention matches kvq_decode_attn over the appended
  * cache.
  *
- * q:      [B, Hq, 1, D] (bf16 or fp16), element strides q_strides[4].
+ * q:      [B, Hq, 1, D] (bf16, fp16 or fp32), element strides q_strides[4].
  * k_new, v_new: [B, Hkv, 1, D] in q's dtype, element strides [4] with unit
- *         inner stride and 4-byte aligned rows.
+ *         inner stride, even batch/head strides and rows aligned to two
+ *         elements (4 bytes for bf16/fp16, 8 for fp32).
  * k_packed/v_packed [B, Hkv, capacity, G*groups/2] uint8 and k_scales/
- * v_scales [B, Hkv, capacity, groups] (16-bit scale_dtype), byte / element
- * strides [3]: the cache buffers. Sequence b's old length is positions[b]
+ * v_scales [B, Hkv, capacity, groups] (scale_dtype bf16, fp16 or fp32),
+ * byte / element strides [3]: the cache buffers. bf16/fp16 queries with
+ * 16-bit scales run on the matrix cores, the rest on the fp32 VALU kernel. Sequence b's old length is positions[b]
  * (device int32 [B]) or pos0 for every sequence; its new row is written at
  * that index and it attends old length + 1 keys. A sequence whose old length
  * is not below `capacity` is left unchanged and attends its first `capacity`

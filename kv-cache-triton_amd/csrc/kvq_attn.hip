@@ -1447,6 +1447,9 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   __shared__ float o_lds[4][ROWS][D];
   __shared__ __attribute__((aligned(16))) float ml_lds[4][ROWS][2];
   __shared__ MergeLds<256> mg;
+  // the decode step's new token: its score per row, then its dequantized
+  // values (two elements per lane of the V wave)
+  __shared__ __attribute__((aligned(16))) float nt_lds[ROWS + 128];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1456,10 +1459,30 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   int b, kvh, rc;
   unit_coords(a, unit, b, kvh, rc);
 
-  int L = a.Sk;
-  if (a.seq_lens) {
-    const int sl = a.seq_lens[b];
-    L = sl < 0 ? 0 : (sl < a.Sk ? sl : a.Sk);
+  int L = !ROWMASK && a.append ? a.pos0 : a.Sk;
+  if (a.seq_lens) L = a.seq_lens[b];
+  L = L < 0 ? 0 : L;
+  // decode step: the new token goes to row L (if it fits the cache) and is
+  // attended by the unit's last split: wave 3 quantizes, stores and scores
+  // its K row, wave 2 quantizes and stores its V row (lane l: elements 2l,
+  // 2l+1, loaded here, ahead of the tiles). A decode step has one query
+  // position, so it never takes the row-masked instances.
+  const bool has_new = !ROWMASK && a.append && L < a.Sk && split == a.n_split - 1;
+  L = L < a.Sk ? L : a.Sk;
+  float nx0 = 0.0f, nx1 = 0.0f;
+  if (has_new && wave >= 2 && lane < D / 2) {
+    const bool is_k = wave == 3;  // wave-uniform
+    const int64_t off = (int64_t)b * (is_k ? a.kns_b : a.vns_b) + (int64_t)kvh * (is_k ? a.kns_h : a.vns_h) +
+                        2 * lane;
+    if constexpr (QM == KVQ_F32) {
+      const float2 x = *(const float2*)((const float*)(is_k ? a.knew : a.vnew) + off);
+      nx0 = x.x;
+      nx1 = x.y;
+    } else {
+      const uint32_t x = *(const uint32_t*)((const uint16_t*)(is_k ? a.knew : a.vnew) + off);
+      nx0 = QM == KVQ_F16 ? f16_bits_to_f32(x & 0xffffu) : bf16_bits_to_f32(x & 0xffffu);
+      nx1 = QM == KVQ_F16 ? f16_bits_to_f32(x >> 16) : bf16_bits_to_f32(x >> 16);
+    }
   }
   int t_begin, t_end;
   split_range(a, L, split, t_begin, t_end);
@@ -1535,6 +1558,75 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   const uint32_t kps = (uint32_t)a.kps_s, vps = (uint32_t)a.vps_s;
   const uint32_t kss = (uint32_t)a.kss_s, vss = (uint32_t)a.vss_s;
   const int last_tok = L > 0 ? L - 1 : 0;
+
+  // decode step: quantize the new K or V row exactly as the quantize kernel
+  // does (group absmax / 7 in fp32, round half to even, clamp, +8; the scale
+  // stored in the cache's scale dtype) and store it at row L. The K wave then
+  // scores the key dequantized with the stored scale against the query rows
+  // (exact fp32), the V wave leaves the dequantized values in LDS; the
+  // workgroup fold takes them in as one more partial.
+  if (has_new && wave >= 2) {  // wave-uniform
+    const bool is_k = wave == 3;
+    const int G = a.G;
+    const int W = ((D + G - 1) / G) * (G / 2);
+    const bool col_ok = lane < D / 2;
+    const bool byte_ok = lane < W;
+    const float x0 = col_ok ? nx0 : 0.0f, x1 = col_ok ? nx1 : 0.0f;
+    float am = row16_max(fmax_nc(fabsf(x0), fabsf(x1)));  // group absmax: G / 2 lanes
+    if (G >= 64) {
+      float u = am, v = am;
+      permlane16_swap(u, v);
+      am = fmax_nc(u, v);
+    }
+    if (G >= 128) {
+      float u = am, v = am;
+      permlane32_swap(u, v);
+      am = fmax_nc(u, v);
+    }
+    const float scale = am > 0.0f ? am / 7.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
+    float c0 = rint_quotient(x0, scale, inv, fast), c1 = rint_quotient(x1, scale, inv, fast);
+    c0 = fminf(fmaxf(c0, -8.0f), 7.0f);
+    c1 = fminf(fmaxf(c1, -8.0f), 7.0f);
+    const uint32_t byte = (uint32_t)((int)c0 + 8) | ((uint32_t)((int)c1 + 8) << 4);
+    uint8_t* prow = const_cast<uint8_t*>(is_k ? kp_bh : vp_bh) + (int64_t)L * (is_k ? kps : vps);
+    char* srow = const_cast<char*>(is_k ? ks_bh : vs_bh) + (int64_t)L * (is_k ? kss : vss) * s_esize;
+    if (byte_ok) prow[lane] = (uint8_t)byte;
+    float sq = scale;
+    const bool scale_lane = byte_ok && (2 * lane) % G == 0;
+    if (a.scale_dtype == KVQ_F32) {
+      if (scale_lane) ((float*)srow)[(2 * lane) / G] = scale;
+    } else {
+      const bool h = a.scale_dtype == KVQ_F16;
+      const uint32_t sbits = h ? f32_to_f16_bits(scale) : f32_to_bf16_bits(scale);
+      if (scale_lane) ((uint16_t*)srow)[(2 * lane) / G] = (uint16_t)sbits;
+      sq = scale16_to_f32(sbits, h);
+    }
+    const float d0 = c0 * sq, d1 = c1 * sq;
+    if (is_k) {
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r) {
+        const int rho = rc * ROWS + r;
+        const bool row_ok = rho < a.rows_total;
+        const int rho_c = row_ok ? rho : 0;
+        const int hq = (int)fdiv((uint32_t)rho_c, a.div_sq);
+        const int head = kvh * a.ratio + hq;
+        const int qi = rho_c - hq * a.Sq;
+        const int64_t qbase = (int64_t)b * a.qs_b + (int64_t)head * a.qs_h + (int64_t)qi * a.qs_s;
+        float part = 0.0f;
+        if (col_ok) {
+          const float q0 = load_as_f32(a.q, qbase + (int64_t)(2 * lane) * a.qs_d, QM);
+          const float q1 = load_as_f32(a.q, qbase + (int64_t)(2 * lane + 1) * a.qs_d, QM);
+          part = fmaf(q0, d0, q1 * d1);
+        }
+        const float sc = wave_sum(part) * a.scale_log2;
+        if (lane == 0) nt_lds[r] = row_ok ? sc : kNeg;
+      }
+    } else {
+      *(float2*)&nt_lds[ROWS + 2 * lane] = make_float2(d0, d1);
+    }
+  }
 
   for (int base = wave; base < ntiles; base += 4 * CH) {
     // tiles of this chunk the wave has (wave-uniform): a split's last chunk
@@ -1716,7 +1808,9 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     }
   }
   __syncthreads();
-  finish_block<ROWS, D, QM, 4>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg);
+  // the new token (scores and values in LDS, written by waves 3 and 2 before
+  // their tile loops) joins the waves' partials in the workgroup fold
+  finish_block<ROWS, D, QM, 4>(a, unit, split, rc, kvh, b, o_lds, ml_lds, mg, has_new ? nt_lds : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -2145,8 +2239,8 @@ static int decode_step_impl(const void* q, int q_dtype, const int64_t* q_strides
                             void* stream, const PagedArgs* pg) {
   KVQ_CHECK_ARG(dtype_ok(q_dtype) && dtype_ok(scale_dtype), "kvq_decode_step: bad dtype");
   KVQ_CHECK_ARG(kn_strides && vn_strides && q_strides, "kvq_decode_step: null stride array");
-  if (!use_mfma(q_dtype, scale_dtype) || !(group_size == 32 || group_size == 64 || group_size == 128)) {
-    set_error("kvq_decode_step: needs bf16/fp16 queries, 16-bit scales and group_size in {32, 64, 128}");
+  if (!(group_size == 32 || group_size == 64 || group_size == 128)) {
+    set_error("kvq_decode_step: needs group_size in {32, 64, 128} (got %lld)", (long long)group_size);
     return KVQ_EUNSUP;
   }
   KVQ_CHECK_ARG(capacity >= 1, "kvq_decode_step: capacity must be >= 1");
@@ -2155,12 +2249,16 @@ static int decode_step_impl(const void* q, int q_dtype, const int64_t* q_strides
                 (long long)capacity);
   if (B == 0) return KVQ_OK;
   KVQ_CHECK_ARG(k_new && v_new, "kvq_decode_step: null new K/V");
-  const bool kn_ok = kn_strides[3] == 1 && (uintptr_t)k_new % 4 == 0 && kn_strides[0] % 2 == 0 &&
+  // a lane loads two consecutive elements of a new row: 4 bytes (16-bit
+  // rows) or 8 bytes (fp32 rows)
+  const int64_t pair = q_dtype == KVQ_F32 ? 8 : 4;
+  const bool kn_ok = kn_strides[3] == 1 && (uintptr_t)k_new % pair == 0 && kn_strides[0] % 2 == 0 &&
                      kn_strides[1] % 2 == 0;
-  const bool vn_ok = vn_strides[3] == 1 && (uintptr_t)v_new % 4 == 0 && vn_strides[0] % 2 == 0 &&
+  const bool vn_ok = vn_strides[3] == 1 && (uintptr_t)v_new % pair == 0 && vn_strides[0] % 2 == 0 &&
                      vn_strides[1] % 2 == 0;
   if (!kn_ok || !vn_ok) {
-    set_error("kvq_decode_step: new K/V rows need unit inner stride and 4-byte alignment");
+    set_error("kvq_decode_step: new K/V rows need unit inner stride and %lld-byte aligned element pairs",
+              (long long)pair);
     return KVQ_EUNSUP;
   }
   const StepArgs step{k_new, kn_strides, v_new, vn_strides, pos0};

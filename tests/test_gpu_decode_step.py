@@ -139,8 +139,113 @@ def test_decode_step_rejects_bad_position_and_unsupported():
     q, kn, vn = _new(B, Hq, Hkv, D, "bf16", seed=3)
     with pytest.raises(ValueError):
         ops.decode_step(q, kn, vn, *a, 64, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
-    with pytest.raises(ops.nat.KVQUnsupported):
-        ops.decode_step(q.float(), kn.float(), vn.float(), *a, 10, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
+    with pytest.raises(ops.nat.KVQUnsupported):  # new rows in another dtype than q
+        ops.decode_step(q, kn.float(), vn.float(), *a, 10, n_kv_heads=Hkv, group_size=G, sm_scale=1.0)
+
+
+# The fp32 VALU kernel's decode step: fp32 queries (exact fp32 arithmetic) or
+# fp32 scales. Codes and scales bit-identical to kvq_quantize's; attention
+# within 1e-4 of the two-launch path and of the float64 oracle for fp32
+# queries (the new key is folded in exact fp32 in both), and within the
+# 16-bit bound for bf16/fp16 queries (outputs rounded to the query dtype).
+TDT32 = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _cache_dt(B, Hkv, cap, D, G, xdt, sdt, n_fill, seed):
+    g = torch.Generator().manual_seed(seed)
+    W, NG = ops.packed_width(D, G), ops.num_groups(D, G)
+    kp = torch.zeros(B, Hkv, cap, W, dtype=torch.uint8, device=DEV)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(B, Hkv, cap, NG, dtype=TDT32[sdt], device=DEV)
+    vs = torch.zeros_like(ks)
+    if n_fill:
+        k = torch.randn(B, Hkv, n_fill, D, generator=g).to(TDT32[xdt]).to(DEV)
+        v = torch.randn(B, Hkv, n_fill, D, generator=g).to(TDT32[xdt]).to(DEV)
+        ops.quantize_into(k, kp, ks, G, 0)
+        ops.quantize_into(v, vp, vs, G, 0)
+    return [kp, ks, vp, vs]
+
+
+def _new_dt(B, Hq, Hkv, D, xdt, seed):
+    g = torch.Generator().manual_seed(seed + 1000)
+    t = TDT32[xdt]
+    q = torch.randn(B, Hq, 1, D, generator=g).to(t).to(DEV)
+    kn = (3.0 * torch.randn(B, Hkv, 1, D, generator=g)).to(t).to(DEV)
+    vn = torch.randn(B, Hkv, 1, D, generator=g).to(t).to(DEV)
+    return q, kn, vn
+
+
+def _close_dt(got, want, xdt):
+    if xdt != "f32":
+        _close(got, want)
+        return
+    g, w = got.cpu().numpy(), want.cpu().numpy()
+    assert np.all(np.abs(g - w) <= 1e-4 + 1e-4 * np.abs(w)), np.abs(g - w).max()
+
+
+VALU_CASES = [
+    # B, Hq, Hkv, D, G, pos, query/new-row dtype, scale dtype
+    (1, 12, 12, 64, 32, 1023, "f32", "f32"),   # GPT-2 small decode shape
+    (2, 12, 12, 64, 64, 300, "f32", "f32"),
+    (1, 32, 8, 128, 32, 4096, "f32", "f32"),   # 4 query heads per KV head: 2 rows per workgroup
+    (1, 32, 8, 128, 32, 1, "f32", "f32"),
+    (1, 8, 2, 128, 128, 513, "f32", "bf16"),
+    (1, 8, 2, 128, 32, 70, "f32", "f16"),
+    (1, 4, 4, 64, 128, 65, "f32", "f32"),      # G > D: padded group
+    (2, 32, 8, 128, 32, 2000, "bf16", "f32"),  # 16-bit queries with fp32 scales
+    (1, 16, 4, 64, 64, 100, "f16", "f32"),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,G,pos,xdt,sdt", VALU_CASES)
+def test_valu_decode_step_matches_append_then_attend(B, Hq, Hkv, D, G, pos, xdt, sdt):
+    print(f"valu decode step: B {B} Hq {Hq} Hkv {Hkv} D {D} G {G} pos {pos} {xdt}/{sdt}", flush=True)
+    cap = pos + 8
+    a = _cache_dt(B, Hkv, cap, D, G, xdt, sdt, pos, seed=pos + D + 5)
+    b = [t.clone() for t in a]
+    q, kn, vn = _new_dt(B, Hq, Hkv, D, xdt, seed=pos + 3)
+    sm = D ** -0.5
+    ops.quantize_into(kn, a[0], a[1], G, pos)
+    ops.quantize_into(vn, a[2], a[3], G, pos)
+    n = pos + 1
+    want = ops.fused_decode_attention(q, a[0][:, :, :n], a[1][:, :, :n], a[2][:, :, :n], a[3][:, :, :n],
+                                      n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm)
+    got = ops.decode_step(q, kn, vn, b[0], b[1], b[2], b[3], pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):  # the whole buffers: new row bit-identical, nothing else touched
+        assert torch.equal(x, y)
+    exact = O.attention_over_quantized(
+        q.float().cpu().numpy(), a[0][:, :, :n].cpu().numpy(), a[1][:, :, :n].float().cpu().numpy(),
+        a[2][:, :, :n].cpu().numpy(), a[3][:, :, :n].float().cpu().numpy(), group_size=G, scale=sm)
+    tol = 1e-4 if xdt == "f32" else 2e-2
+    assert np.abs(got.float().cpu().numpy() - exact).max() <= tol
+    _close_dt(got, want, xdt)
+
+
+def test_valu_decode_step_ragged_positions_and_full_sequence():
+    """Per-sequence positions on the fp32 kernel, one of them at capacity
+    (not written; attends the keys it has), with the split count forced up so
+    the new token lands in the last of several splits."""
+    print("valu decode step: ragged positions", flush=True)
+    B, Hq, Hkv, D, G, cap = 4, 12, 12, 64, 32, 1100
+    b = _cache_dt(B, Hkv, cap, D, G, "f32", "f32", cap, seed=17)
+    pos = torch.tensor([1000, 0, cap, 517], dtype=torch.int32, device=DEV)
+    q, kn, vn = _new_dt(B, Hq, Hkv, D, "f32", seed=17)
+    sm = D ** -0.5
+    ref = [t.clone() for t in b]
+    for i, p in enumerate(pos.tolist()):
+        if p < cap:  # the two-launch path writes in bounds only (views of one sequence)
+            ops.quantize_into(kn[i:i + 1], ref[0][i:i + 1], ref[1][i:i + 1], G, p)
+            ops.quantize_into(vn[i:i + 1], ref[2][i:i + 1], ref[3][i:i + 1], G, p)
+    lens = torch.clamp(pos + 1, max=cap)
+    want = ops.fused_decode_attention(q, ref[0], ref[1], ref[2], ref[3], n_kv_heads=Hkv, group_size=G,
+                                      is_causal=False, sm_scale=sm, seq_lens=lens)
+    got = ops.decode_step(q, kn, vn, b[0], b[1], b[2], b[3], pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm,
+                          n_split=4)
+    torch.cuda.synchronize()
+    for x, y in zip(ref, b):
+        assert torch.equal(x, y)
+    _close_dt(got, want, "f32")
 
 
 def test_decode_step_in_hip_graph_replays():
