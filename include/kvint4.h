@@ -67,13 +67,16 @@ const char* kvq_last_error(void);
  *           strides scale_strides[3] (b, h, s); last dim contiguous.
  * Row (b, h, s) of x is written to destination row (b, h, pos_b + s) where
  * pos_b = write_pos[b] when write_pos (device int32 [B]) is not NULL, else
- * write_pos0. The caller guarantees the destination rows exist.
+ * write_pos0. capacity = the destination's rows per (b, h): with write_pos
+ * NULL, write_pos0 + S > capacity is rejected (KVQ_EINVAL) before any launch;
+ * with device positions, rows that land at or past capacity (or below 0) are
+ * dropped, as the decode step drops a token past the capacity.
  */
 int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides,
                  int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
                  void* packed, const int64_t* packed_strides,
                  void* scales, int scale_dtype, const int64_t* scale_strides,
-                 const int32_t* write_pos, int64_t write_pos0,
+                 const int32_t* write_pos, int64_t write_pos0, int64_t capacity,
                  void* stream);
 
 /*

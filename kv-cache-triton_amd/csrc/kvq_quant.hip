@@ -15,6 +15,7 @@
 // groups of the same row, which keeps the global accesses of a wave dense.
 
 #include <algorithm>
+#include <limits>
 
 #include "kvq_common.h"
 
@@ -31,14 +32,16 @@ struct QuantArgs {
   int64_t ss_b, ss_h, ss_s;         // element strides of scales
   const int32_t* write_pos;
   int64_t write_pos0;
+  int64_t cap;  // contiguous layout: destination rows per (b, h); rows at or past it are dropped
   int x_dtype, scale_dtype;
   PageMap pm;  // pm.paged: packed/scales are pools (ps_b = ss_b = 0)
 };
 
-// Destination row of (b, position) and whether it exists: the position
-// itself in the contiguous layout, its pool row in the paged one.
+// Destination row of (b, position), or -1 where it does not exist: the
+// position itself in the contiguous layout (if inside [0, cap)), its pool row
+// in the paged one.
 __device__ __forceinline__ int64_t dest_row(const QuantArgs& a, int64_t b, int64_t pos) {
-  return a.pm.paged ? page_row(a.pm, b, pos) : pos;
+  return a.pm.paged ? page_row(a.pm, b, pos) : (pos >= 0 && pos < a.cap ? pos : -1);
 }
 
 template <int XDT>
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
   const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
 
   const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s);
-  if (pos < 0) return;  // paged: no block holds this position
+  if (pos < 0) return;  // no destination row: past the capacity, or no block holds it
   uint8_t* prow = a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + g * a.bpg;
 
   for (int64_t j = 0; j < a.bpg; ++j) {
@@ -163,8 +166,12 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) pos[k] = a.write_pos0 + ss[k];
   }
-  int64_t dst[RPT];  // destination row; < 0: paged, no block holds it
+  int64_t dst[RPT];  // destination row; < 0: none (past the capacity, or no block holds it)
   page_rows<RPT>(a.pm, bb, pos, dst);
+  if (!a.pm.paged) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) dst[k] = dst[k] < a.cap ? dst[k] : -1;
+  }
   float x[RPT][8];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
       word |= (uint32_t)((int)qf + 8) << (4 * e);
     }
     const int64_t b = bb[k], h = hh[k], pos = dst[k];
-    if (pos < 0) continue;  // paged: no block holds this position
+    if (pos < 0) continue;  // no destination row
     // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
     *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
     if (ch % LPG == 0) {
@@ -396,14 +403,18 @@ int quantize_impl(const char* who, const void* x, int x_dtype, const int64_t* x_
                   int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
                   void* packed, const int64_t* packed_strides,
                   void* scales, int scale_dtype, const int64_t* scale_strides,
-                  const int32_t* write_pos, int64_t write_pos0, const PageMap& pm,
-                  void* stream) {
+                  const int32_t* write_pos, int64_t write_pos0, int64_t capacity,
+                  const PageMap& pm, void* stream) {
   KVQ_CHECK_ARG(group_size > 0, "kvq_quantize: group_size must be > 0");
   KVQ_CHECK_ARG(dtype_ok(x_dtype), "kvq_quantize: x dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(dtype_ok(scale_dtype), "kvq_quantize: scale dtype must be bf16/fp16/fp32");
   KVQ_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D >= 0, "kvq_quantize: negative extent");
   KVQ_CHECK_ARG(x_strides && packed_strides && scale_strides, "kvq_quantize: null stride array");
   KVQ_CHECK_ARG(write_pos0 >= 0, "kvq_quantize: write_pos0 must be >= 0");
+  KVQ_CHECK_ARG(capacity >= 0, "kvq_quantize: capacity must be >= 0");
+  KVQ_CHECK_ARG(write_pos != nullptr || B * H * S == 0 || write_pos0 + S <= capacity,
+                "kvq_quantize: rows %lld..%lld outside the destination's %lld rows", (long long)write_pos0,
+                (long long)(write_pos0 + S - 1), (long long)capacity);
   const int64_t rows = B * H * S;
   const int64_t ngroups = (D + group_size - 1) / group_size;
   if (rows == 0 || ngroups == 0) return KVQ_OK;
@@ -421,6 +432,7 @@ int quantize_impl(const char* who, const void* x, int x_dtype, const int64_t* x_
   a.scales = scales;
   a.ss_b = scale_strides[0]; a.ss_h = scale_strides[1]; a.ss_s = scale_strides[2];
   a.write_pos = write_pos; a.write_pos0 = write_pos0;
+  a.cap = capacity;
   a.x_dtype = x_dtype; a.scale_dtype = scale_dtype;
   a.pm = pm;
 
@@ -518,13 +530,13 @@ extern "C" int kvq_quantize(const void* x, int x_dtype, const int64_t* x_strides
                             int64_t B, int64_t H, int64_t S, int64_t D, int64_t group_size,
                             void* packed, const int64_t* packed_strides,
                             void* scales, int scale_dtype, const int64_t* scale_strides,
-                            const int32_t* write_pos, int64_t write_pos0,
+                            const int32_t* write_pos, int64_t write_pos0, int64_t capacity,
                             void* stream) {
   clear_error();
   const PageMap pm{0, nullptr, 0, 0, 0, 0};
   return quantize_impl("kvq_quantize", x, x_dtype, x_strides, B, H, S, D, group_size, packed,
-                       packed_strides, scales, scale_dtype, scale_strides, write_pos, write_pos0, pm,
-                       stream);
+                       packed_strides, scales, scale_dtype, scale_strides, write_pos, write_pos0, capacity,
+                       pm, stream);
 }
 
 extern "C" int kvq_quantize_paged(const void* x, int x_dtype, const int64_t* x_strides,
@@ -544,7 +556,8 @@ extern "C" int kvq_quantize_paged(const void* x, int x_dtype, const int64_t* x_s
   const int64_t ps[3] = {0, pool_strides[0], pool_strides[1]};
   const int64_t ss[3] = {0, scale_pool_strides[0], scale_pool_strides[1]};
   return quantize_impl("kvq_quantize_paged", x, x_dtype, x_strides, B, H, S, D, group_size,
-                       packed_pool, ps, scale_pool, scale_dtype, ss, write_pos, write_pos0, pm, stream);
+                       packed_pool, ps, scale_pool, scale_dtype, ss, write_pos, write_pos0,
+                       std::numeric_limits<int64_t>::max(), pm, stream);
 }
 
 extern "C" int kvq_dequantize(const void* packed, const int64_t* packed_strides,

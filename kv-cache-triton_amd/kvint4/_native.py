@@ -62,7 +62,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.kvq_quantize.restype = _i32
     lib.kvq_quantize.argtypes = [
         _vp, _i32, _i64p, _i64, _i64, _i64, _i64, _i64,
-        _vp, _i64p, _vp, _i32, _i64p, _vp, _i64, _vp,
+        _vp, _i64p, _vp, _i32, _i64p, _vp, _i64, _i64, _vp,
     ]
     lib.kvq_dequantize.restype = _i32
     lib.kvq_dequantize.argtypes = [

@@ -96,8 +96,9 @@ def quantize_into(
     """Quantize x [B, H, S, D] and write the rows at positions pos_b + s of the
     cache tensors packed [B, H, S_cap, W] / scales [B, H, S_cap, n_groups].
 
-    `write_pos` is an int (same position for every batch row) or a device int32
-    tensor [B] of per-sequence positions.
+    `write_pos` is an int (same position for every batch row; rows past the
+    cache's capacity raise ValueError) or a device int32 tensor [B] of
+    per-sequence positions (rows past the capacity are dropped).
     """
     _check_cuda(x, packed, scales, what="quantize_into")
     if x.dim() != 4 or packed.dim() != 4 or scales.dim() != 4:
@@ -128,7 +129,7 @@ def quantize_into(
             B, H, S, D, group_size,
             packed.data_ptr(), nat.i64_array(packed.stride()[:3]),
             scales.data_ptr(), nat.DTYPE_CODE[scales.dtype], nat.i64_array(scales.stride()[:3]),
-            wp_ptr, wp0, nat.stream_handle(x.device),
+            wp_ptr, wp0, min(int(packed.shape[2]), int(scales.shape[2])), nat.stream_handle(x.device),
         )
     nat.check(rc, "kvq_quantize")
 
@@ -153,7 +154,7 @@ def quantize(x: torch.Tensor, group_size: int, scale_dtype: torch.dtype) -> tupl
             sizes[0], sizes[1], sizes[2], d, group_size,
             pv.data_ptr(), nat.i64_array(pv.stride()[:3]),
             sv.data_ptr(), nat.DTYPE_CODE[scale_dtype], nat.i64_array(sv.stride()[:3]),
-            None, 0, nat.stream_handle(x.device),
+            None, 0, sizes[2], nat.stream_handle(x.device),
         )
     nat.check(rc, "kvq_quantize")
     return packed, scales

@@ -79,13 +79,20 @@ def test_invalid_arguments_rejected_before_any_launch():
     s4 = nat.i64_array([0, 0, 0, 1])
     s3 = nat.i64_array([0, 0, 0])
     rc = lib.kvq_quantize(None, nat.KVQ_BF16, s4, 1, 1, 1, 128, 0, None, s3, None, nat.KVQ_BF16, s3,
-                          None, 0, None)
+                          None, 0, 1, None)
     assert rc == nat.KVQ_EINVAL and "group_size" in nat.last_error()
-    rc = lib.kvq_quantize(None, 9, s4, 1, 1, 1, 128, 32, None, s3, None, nat.KVQ_BF16, s3, None, 0, None)
+    rc = lib.kvq_quantize(None, 9, s4, 1, 1, 1, 128, 32, None, s3, None, nat.KVQ_BF16, s3, None, 0, 1, None)
     assert rc == nat.KVQ_EINVAL and "dtype" in nat.last_error()
     rc = lib.kvq_quantize(None, nat.KVQ_BF16, s4, 1, 1, 1, 128, 32, None, s3, None, nat.KVQ_BF16, s3,
-                          None, 0, None)
+                          None, 0, 1, None)
     assert rc == nat.KVQ_EINVAL and "null" in nat.last_error()
+    # a scalar position whose rows do not fit the destination, and a negative capacity
+    rc = lib.kvq_quantize(None, nat.KVQ_BF16, s4, 1, 1, 3, 128, 32, None, s3, None, nat.KVQ_BF16, s3,
+                          None, 8, 10, None)
+    assert rc == nat.KVQ_EINVAL and "outside the destination" in nat.last_error()
+    rc = lib.kvq_quantize(None, nat.KVQ_BF16, s4, 1, 1, 1, 128, 32, None, s3, None, nat.KVQ_BF16, s3,
+                          None, 0, -1, None)
+    assert rc == nat.KVQ_EINVAL and "capacity" in nat.last_error()
     rc = lib.kvq_dequantize(None, s3, None, nat.KVQ_BF16, s3, 1, 1, 1, 32, 4, None, nat.KVQ_BF16, s4,
                             200, None)
     assert rc == nat.KVQ_EINVAL and "d_out" in nat.last_error()

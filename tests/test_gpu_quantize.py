@@ -134,6 +134,35 @@ def test_append_in_place_scalar_and_ragged_positions():
         assert np.array_equal(O.bits(_np(ks[b, :, p0:p0 + 2]), "bf16"), O.bits(s2[b], "bf16"))
 
 
+@pytest.mark.parametrize("G", [32, 33])  # the vector kernel and the general one
+def test_append_drops_rows_past_the_capacity(G):
+    """Device positions: rows that land at or past the capacity are dropped,
+    the rest written bit-exact. The destination is a view of a taller buffer,
+    so a row written past the capacity would land in the (zero) rows below it
+    rather than outside the allocation."""
+    print(f"quantize past capacity: G {G}", flush=True)
+    B, H, D, cap, S, pad = 4, 2, 128, 64, 4, 16
+    W, NG = ops.packed_width(D, G), ops.num_groups(D, G)
+    kp_full = torch.zeros(B, H, cap + pad, W, dtype=torch.uint8, device=DEV)
+    ks_full = torch.zeros(B, H, cap + pad, NG, dtype=torch.bfloat16, device=DEV)
+    kp, ks = kp_full[:, :, :cap], ks_full[:, :, :cap]
+    starts = [62, 64, 70, 30]
+    x = _config_tensor((B, H, S, D), "bf16", None, seed=9)
+    ops.quantize_into(x.to(DEV), kp, ks, G, torch.tensor(starts, dtype=torch.int32, device=DEV))
+    p, sc = O.quantize_int4(x.float().numpy(), G, "bf16")
+    got_p, got_s = kp_full.cpu().numpy(), O.bits(_np(ks_full), "bf16")
+    want_s = O.bits(sc, "bf16")
+    for b, p0 in enumerate(starts):
+        n = max(0, min(S, cap - p0))  # rows that fit
+        assert np.array_equal(got_p[b, :, p0:p0 + n], p[b, :, :n])
+        assert np.array_equal(got_s[b, :, p0:p0 + n], want_s[b, :, :n])
+        rest = np.ones(cap + pad, dtype=bool)
+        rest[p0:p0 + n] = False
+        assert (got_p[b][:, rest] == 0).all() and (got_s[b][:, rest] == 0).all()
+    with pytest.raises(ValueError):  # a scalar position whose rows do not fit
+        ops.quantize_into(x.to(DEV), kp, ks, G, 61)
+
+
 def test_reference_properties():
     # tests/llama3/test_quantize.py:57-83, tests/gpt2/test_quantize.py:25-40
     x = torch.randn(1, 4, 16, 128, device=DEV, dtype=torch.bfloat16)
