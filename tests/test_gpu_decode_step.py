@@ -248,6 +248,36 @@ def test_valu_decode_step_ragged_positions_and_full_sequence():
     _close_dt(got, want, "f32")
 
 
+def test_valu_decode_step_in_hip_graph_replays():
+    """The fp32 kernel's decode step captured in a HIP graph: every replay
+    (eager work and synchronisation between them) gives the eager result and
+    the same cache bytes (its split counters re-armed by the kernel)."""
+    print("valu decode step in a HIP graph", flush=True)
+    B, Hq, Hkv, D, G, pos = 1, 12, 12, 64, 32, 1000
+    a = _cache_dt(B, Hkv, pos + 8, D, G, "f32", "f32", pos, seed=23)
+    q, kn, vn = _new_dt(B, Hq, Hkv, D, "f32", seed=23)
+    sm = D ** -0.5
+    out = torch.empty_like(q)
+    ops.decode_step(q, kn, vn, *a, pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm, out=out)  # warm-up
+    torch.cuda.synchronize()
+    want = out.clone()
+    cache_want = [t.clone() for t in a]
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        ops.decode_step(q, kn, vn, *a, pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm, out=out)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        out.zero_()
+        (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        for x, y in zip(a, cache_want):
+            assert torch.equal(x, y)
+
+
 def test_decode_step_in_hip_graph_replays():
     """The decode step captured in a HIP graph: every replay (with eager work
     and synchronisation between them) gives the eager result and the same
