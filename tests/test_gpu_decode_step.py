@@ -365,3 +365,60 @@ def test_decode_steps_of_several_layers_in_one_graph_advance_device_positions(D,
         assert torch.equal(pos_g[l], pos_e[l])
         for a, b in zip(caches_e[l], caches_g[l]):
             assert torch.equal(a, b)
+
+
+def _random_step_case(seed):
+    r = np.random.default_rng(seed)
+    xdt = ["bf16", "f16", "f32"][r.integers(3)]
+    sdt = ["bf16", "f16", "f32"][r.integers(3)]
+    B = int(r.integers(1, 4))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    ratio = int(r.choice([1, 2, 4, 8]))
+    D = int(r.choice([64, 128]))
+    G = int(r.choice([32, 64, 128]))
+    cap = int(r.integers(40, 2500))
+    pos = [int(r.integers(0, cap)) for _ in range(B)]
+    if B > 1 and r.random() < 0.5:
+        pos[int(r.integers(B))] = cap  # a full sequence: not written, attends its cap keys
+    n_split = None if r.random() < 0.5 else int(r.integers(1, 9))
+    return xdt, sdt, B, Hkv, ratio, D, G, cap, pos, n_split
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_decode_step_random_shapes(seed):
+    """Seeded random decode steps over both kernels (query and scale dtypes),
+    GQA ratios, head dims, group sizes, per-sequence positions (one may be at
+    the capacity) and forced split counts: cache bytes bit-identical to the
+    two-launch route, output within its bar, and within the oracle's bar."""
+    xdt, sdt, B, Hkv, ratio, D, G, cap, pos, n_split = _random_step_case(seed)
+    Hq = Hkv * ratio
+    print(f"random decode step {seed}: {xdt}/{sdt} B {B} Hq {Hq} Hkv {Hkv} D {D} G {G} cap {cap} "
+          f"pos {pos} n_split {n_split}", flush=True)
+    b = _cache_dt(B, Hkv, cap, D, G, xdt, sdt, cap, seed=300 + seed)
+    q, kn, vn = _new_dt(B, Hq, Hkv, D, xdt, seed=300 + seed)
+    sm = D ** -0.5
+    ref = [t.clone() for t in b]
+    for i, p in enumerate(pos):
+        if p < cap:
+            ops.quantize_into(kn[i:i + 1], ref[0][i:i + 1], ref[1][i:i + 1], G, p)
+            ops.quantize_into(vn[i:i + 1], ref[2][i:i + 1], ref[3][i:i + 1], G, p)
+    pos_t = torch.tensor(pos, dtype=torch.int32, device=DEV)
+    lens = torch.clamp(pos_t + 1, max=cap)
+    want = ops.fused_decode_attention(q, ref[0], ref[1], ref[2], ref[3], n_kv_heads=Hkv, group_size=G,
+                                      is_causal=False, sm_scale=sm, seq_lens=lens)
+    if n_split is not None:
+        n_split = max(1, min(n_split, cap // 128))
+    got = ops.decode_step(q, kn, vn, b[0], b[1], b[2], b[3], pos_t, n_kv_heads=Hkv, group_size=G,
+                          sm_scale=sm, n_split=n_split)
+    torch.cuda.synchronize()
+    for x, y in zip(ref, b):
+        assert torch.equal(x, y)
+    _close_dt(got, want, xdt)
+    tol = 1e-4 if xdt == "f32" else 2e-2
+    g = got.float().cpu().numpy()
+    for i, n in enumerate(lens.tolist()):
+        exact = O.attention_over_quantized(
+            q[i:i + 1].float().cpu().numpy(), ref[0][i:i + 1, :, :n].cpu().numpy(),
+            ref[1][i:i + 1, :, :n].float().cpu().numpy(), ref[2][i:i + 1, :, :n].cpu().numpy(),
+            ref[3][i:i + 1, :, :n].float().cpu().numpy(), group_size=G, scale=sm)
+        assert np.abs(g[i:i + 1] - exact).max() <= tol, (i, np.abs(g[i:i + 1] - exact).max())
