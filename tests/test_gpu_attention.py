@@ -227,3 +227,48 @@ def test_validation_errors():
         attention_forward_quant_gqa(q, kp, ks, vp, vs, n_q_heads=8, n_kv_heads=4)
     with pytest.raises(ValueError):
         attention_forward_quant(qd.to(torch.bfloat16), kp, ks, vp, vs)
+
+
+def _random_attn_case(seed):
+    r = np.random.default_rng(1000 + seed)
+    dtype = ["bf16", "f16", "f32"][r.integers(3)]
+    sdt = ["bf16", "f16", "f32"][r.integers(3)]
+    B = int(r.integers(1, 4))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    ratio = int(r.choice([1, 2, 4, 8]))
+    Sq = int(r.choice([1, 1, 2, 3, 5, 8]))
+    causal = bool(r.random() < 0.5) and Sq > 1
+    D = int(r.choice([64, 128]))
+    G = int(r.choice([32, 64, 128]))
+    Sk = int(r.integers(1, 2200))
+    lens = None
+    if r.random() < 0.5:
+        lens = [int(r.integers(0, Sk + 1)) for _ in range(B)]
+    n_split = None if r.random() < 0.5 else int(r.integers(1, 12))
+    return dtype, sdt, B, Hkv, ratio, Sq, causal, D, G, Sk, lens, n_split
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_fused_attention_random_shapes(seed):
+    """Seeded random calls of the fused kernel itself (both kernels by query
+    and scale dtype): multi-token query blocks with and without the
+    bottom-right causal mask (the row-masked instances), GQA ratios that split
+    the rows into several chunks, ragged lengths including 0, forced split
+    counts. Bar: 1e-4 (fp32 queries) or 2e-2 against the float64 oracle."""
+    dtype, sdt, B, Hkv, ratio, Sq, causal, D, G, Sk, lens, n_split = _random_attn_case(seed)
+    Hq = Hkv * ratio
+    print(f"random fused attention {seed}: {dtype}/{sdt} B {B} Hq {Hq} Hkv {Hkv} Sq {Sq} causal {causal} "
+          f"D {D} G {G} Sk {Sk} lens {lens} n_split {n_split}", flush=True)
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, seed=2000 + seed, scale_dtype=sdt, G=G)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV) if lens is not None else None
+    if n_split is not None:
+        n_split = max(1, min(n_split, Sk // 128))
+    sm = D ** -0.5
+    out = ops.fused_decode_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=causal,
+                                     sm_scale=sm, seq_lens=sl, n_split=n_split)
+    got = out.float().cpu().numpy()
+    want = _oracle(q, kp, ks, vp, vs, G, causal=causal, seq_lens=lens, scale=sm)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    assert np.isfinite(got).all()
+    err = np.abs(got - want).max()
+    assert err <= tol, err
