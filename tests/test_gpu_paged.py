@@ -401,3 +401,76 @@ def test_prefill_kernel_paged_matches_contiguous(B, Hq, Hkv, Sq, S, P):
     cache.append(k, v, 0)
     out = cache.attend(q, 0, n_kv_heads=Hkv, scale=D ** -0.5, is_causal=True)
     assert (out.float() - want.float()).abs().max().item() <= 2e-2
+
+
+def _random_paged_case(seed):
+    r = np.random.default_rng(3000 + seed)
+    dtype = ["bf16", "f16"][r.integers(2)]
+    B = int(r.integers(1, 4))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    ratio = int(r.choice([1, 2, 4, 8]))
+    D = int(r.choice([64, 128]))
+    G = int(r.choice([32, 64, 128]))
+    P = int(r.choice([64, 128, 256]))
+    lens = [int(r.integers(1, 1500)) for _ in range(B)]
+    Sq = int(r.choice([1, 1, 2, 4]))
+    causal = Sq > 1 and bool(r.random() < 0.5)
+    return dtype, B, Hkv, ratio, D, G, P, lens, Sq, causal
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_paged_random_shapes(seed):
+    """Seeded random paged caches (page sizes 64-256, permuted block tables,
+    ragged lengths, GQA ratios, D, G, query blocks with and without the causal
+    mask): attention within 2e-2 of the oracle; at one split bit-identical to
+    the contiguous kernel over the gathered rows; for one-token queries the
+    paged decode step writes the quantizer's bytes and matches the
+    contiguous step."""
+    dtype, B, Hkv, ratio, D, G, P, lens, Sq, causal = _random_paged_case(seed)
+    Hq = Hkv * ratio
+    print(f"random paged {seed}: {dtype} B {B} Hq {Hq} Hkv {Hkv} D {D} G {G} P {P} lens {lens} Sq {Sq} "
+          f"causal {causal}", flush=True)
+    t = TDT[dtype]
+    n_blocks = sum(-(-(n + 1) // P) for n in lens) + 2
+    table = _table([n + 1 for n in lens], P, n_blocks, seed=4000 + seed)
+    pt = ops.PageTable(table, P, n_blocks)
+    pools = _pools(Hkv, n_blocks, P, D, G, t)
+    S = max(lens)
+    g = torch.Generator().manual_seed(5000 + seed)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(t)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(t)
+    ops.quantize_into_paged(k.to(DEV), pools[0], pools[1], pt, G, 0)
+    ops.quantize_into_paged(v.to(DEV), pools[2], pools[3], pt, G, 0)
+    q = torch.randn(B, Hq, Sq, D, generator=g).to(t).to(DEV)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    sm = D ** -0.5
+    got = ops.fused_decode_attention_paged(q, *pools, pt, n_kv_heads=Hkv, group_size=G, is_causal=causal,
+                                           sm_scale=sm, seq_lens=sl)
+    cont = [_gather(p, table, P, S).contiguous() for p in pools]
+    exact = O.attention_over_quantized(q.float().cpu().numpy(), *(c.cpu().numpy() if c.dtype == torch.uint8
+                                       else c.float().cpu().numpy() for c in cont),
+                                       group_size=G, scale=sm, is_causal=causal, seq_lens=lens)
+    err = np.abs(got.float().cpu().numpy() - O.round_to(exact.astype(np.float32), dtype)).max()
+    assert err <= 2e-2, err
+    got1 = ops.fused_decode_attention_paged(q, *pools, pt, n_kv_heads=Hkv, group_size=G, is_causal=causal,
+                                            sm_scale=sm, seq_lens=sl, n_split=1)
+    want1 = ops.fused_decode_attention(q, *cont, n_kv_heads=Hkv, group_size=G, is_causal=causal, sm_scale=sm,
+                                       seq_lens=sl, n_split=1)
+    assert torch.equal(got1, want1)
+    if Sq != 1:
+        return
+    kn = (3 * torch.randn(B, Hkv, 1, D, generator=g)).to(t).to(DEV)
+    vn = torch.randn(B, Hkv, 1, D, generator=g).to(t).to(DEV)
+    got_s = ops.decode_step_paged(q, kn, vn, *pools, pt, sl, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    want_kp, want_ks = O.quantize_int4(kn.float().cpu().numpy(), G, dtype)
+    want_vp, want_vs = O.quantize_int4(vn.float().cpu().numpy(), G, dtype)
+    cont = [_gather(p, table, P, S + 1).contiguous() for p in pools]
+    for b, n in enumerate(lens):
+        assert np.array_equal(cont[0][b, :, n].cpu().numpy(), want_kp[b, :, 0])
+        assert np.array_equal(cont[2][b, :, n].cpu().numpy(), want_vp[b, :, 0])
+        assert np.array_equal(O.bits(cont[1][b, :, n].float().cpu().numpy(), dtype), O.bits(want_ks[b, :, 0], dtype))
+        assert np.array_equal(O.bits(cont[3][b, :, n].float().cpu().numpy(), dtype), O.bits(want_vs[b, :, 0], dtype))
+    want_s = ops.fused_decode_attention(q, *cont, n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm,
+                                        seq_lens=sl + 1)
+    g_np, w_np = got_s.float().cpu().numpy(), want_s.float().cpu().numpy()
+    assert np.all(np.abs(g_np - w_np) <= 2.0 ** -6 + 2.0 ** -7 * np.abs(w_np)), np.abs(g_np - w_np).max()
