@@ -113,3 +113,36 @@ def test_prefill_two_row_blocks_per_wave(B):
             q[:, :, i:i + 1].float().numpy(), kp[:, :, :n].cpu().numpy(), ks[:, :, :n].float().cpu().numpy(),
             vp[:, :, :n].cpu().numpy(), vs[:, :, :n].float().cpu().numpy(), group_size=G, is_causal=False)
         assert np.abs(got[:, :, i:i + 1] - want).max() <= 2e-2, i
+
+
+def _random_prefill_case(seed):
+    r = np.random.default_rng(6000 + seed)
+    dtype = ["bf16", "f16"][r.integers(2)]
+    B = int(r.integers(1, 3))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    ratio = int(r.choice([1, 2, 4, 8]))
+    D = int(r.choice([64, 128]))
+    G = min(int(r.choice([32, 64, 128])), D)  # the kernel takes groups that divide D
+    Sk = int(r.integers(1, 2500))
+    Sq = int(r.integers(1, min(Sk, 700) + 1)) if r.random() < 0.8 else int(r.integers(Sk, Sk + 200))
+    causal = bool(r.random() < 0.7)
+    return dtype, B, Hkv, ratio, D, G, Sq, Sk, causal
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_prefill_random_shapes(seed):
+    """Seeded random query blocks on the prefill kernel (GQA ratios, D, G,
+    fp16/bf16, prompts, chunks after cached tokens, more queries than keys,
+    causal or not, launches that split over keys): within 2e-2 of the float64
+    oracle."""
+    dtype, B, Hkv, ratio, D, G, Sq, Sk, causal = _random_prefill_case(seed)
+    Hq = Hkv * ratio
+    print(f"random prefill {seed}: {dtype} B {B} Hq {Hq} Hkv {Hkv} D {D} G {G} Sq {Sq} Sk {Sk} causal {causal}",
+          flush=True)
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, dtype, G, seed=7000 + seed, cap=Sk + 17)
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=causal,
+                                sm_scale=D ** -0.5)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got - _oracle(q, kp, ks, vp, vs, G, causal)).max()
+    assert err <= 2e-2, err
