@@ -184,3 +184,34 @@ def test_reference_properties():
         lq.quantize_int4(torch.randint(0, 5, (4, 128), dtype=torch.int32, device=DEV))
     with pytest.raises(ValueError):
         lq.quantize_int4(torch.randn(4, 128))  # CPU tensors are not served
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_quantize_random_shapes(seed):
+    """Seeded random quantize / dequantize calls: any head dim, group sizes
+    that divide it or not (odd ones included), every input and scale dtype,
+    contiguous or transposed inputs, outlier channels. Codes and scale bits
+    equal the oracle's; dequantized values equal the oracle's bit for bit."""
+    r = np.random.default_rng(8000 + seed)
+    B, H, S = int(r.integers(1, 4)), int(r.integers(1, 6)), int(r.integers(1, 200))
+    D = int(r.integers(1, 257))
+    G = int(r.choice([3, 5, 7, 16, 32, 33, 48, 64, 96, 128, 200]))
+    xdt = ["bf16", "f16", "f32"][r.integers(3)]
+    sdt = ["bf16", "f16", "f32"][r.integers(3)]
+    transposed = bool(r.random() < 0.5)
+    outliers = [int(c) for c in r.choice(D, size=min(D, 3), replace=False)] if r.random() < 0.5 else None
+    print(f"random quantize {seed}: B {B} H {H} S {S} D {D} G {G} {xdt}/{sdt} transposed {transposed} "
+          f"outliers {outliers}", flush=True)
+    g = torch.Generator().manual_seed(9000 + seed)
+    x = torch.randn(*((B, S, H, D) if transposed else (B, H, S, D)), generator=g)
+    if outliers:
+        x[..., outliers] *= 8.0
+    x = x.to(TDT[xdt])
+    xd = x.to(DEV)
+    if transposed:
+        xd, x = xd.transpose(1, 2), x.transpose(1, 2)  # [B, H, S, D] views, not contiguous
+    packed, scales = ops.quantize(xd, G, TDT[sdt])
+    _assert_codes_equal(packed, scales, x.float().numpy(), G, sdt)
+    out = ops.dequantize(packed, scales, G, D, torch.float32)
+    want = O.dequantize_int4(packed.cpu().numpy(), _np(scales), G, D, "f32")
+    assert np.array_equal(_np(out), want)
