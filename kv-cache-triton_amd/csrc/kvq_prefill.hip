@@ -121,8 +121,10 @@ void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int VP = kKeys + 8;  // V^T tile row pitch
   constexpr int NK = D / 32;     // 32-dim steps of S^T
   constexpr int NB = D / 16;     // 16-dim blocks of O^T
-  __shared__ __align__(16) uint16_t k_lds[kKeys * KP];
-  __shared__ __align__(16) uint16_t v_lds[D * VP];
+  // two tile buffers: tile i is read from buffer i % 2 while tile i + 1 is
+  // dequantized into the other one
+  __shared__ __align__(16) uint16_t k_lds[2][kKeys * KP];
+  __shared__ __align__(16) uint16_t v_lds[2][D * VP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane & 15, lg = lane >> 4;
@@ -243,7 +245,7 @@ void prefill_attn_kernel(const PrefillArgs a) {
       vsc[i] = __builtin_amdgcn_raw_buffer_load_b16(tvs, vr * vss2 + 2u * v_grp, 0, 0);
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
     {  // K row k_key, dims k_q * D / 4 .. + D / 4 (element 2j of a byte's pair in the low nibble)
       const float sc = scale_f32<S_F16>(ksc);
       uint32_t pk[KB];
@@ -254,7 +256,7 @@ void prefill_attn_kernel(const PrefillArgs a) {
           const uint32_t byte = (kraw[w] >> (8 * j)) & 0xffu;
           pk[4 * w + j] = pack2<F16>((float)((int)(byte & 15u) - 8) * sc, (float)((int)(byte >> 4) - 8) * sc);
         }
-      uint16_t* dst = k_lds + k_key * KP + k_q * (D / 4);
+      uint16_t* dst = k_lds[buf] + k_key * KP + k_q * (D / 4);
 #pragma unroll
       for (int w = 0; w < KB / 4; ++w)
         *(uint4*)(dst + 8 * w) = make_uint4(pk[4 * w], pk[4 * w + 1], pk[4 * w + 2], pk[4 * w + 3]);
@@ -269,7 +271,7 @@ void prefill_attn_kernel(const PrefillArgs a) {
       }
 #pragma unroll
       for (int d = 0; d < VD; ++d)
-        *(uint2*)(v_lds + (v_dq * VD + d) * VP + 4 * v_kq) =
+        *(uint2*)(v_lds[buf] + (v_dq * VD + d) * VP + 4 * v_kq) =
             make_uint2(pack2<F16>(vf[0][d], vf[1][d]), pack2<F16>(vf[2][d], vf[3][d]));
     }
   };
@@ -284,13 +286,23 @@ void prefill_attn_kernel(const PrefillArgs a) {
     l_run[r] = 0.0f;
   }
 
-  if (tile_lo < tile_hi) load_tile((uint32_t)(tile_lo * kKeys));
+  // Tile i's codes are loaded into registers during tile i - 2, dequantized
+  // into buffer i % 2 during tile i - 1 (after that tile's S^T products are
+  // issued, so the dequantize overlaps them) and read during tile i. One
+  // barrier per tile: at its end every wave has read buffer i % 2 (written
+  // again during tile i + 1) and written buffer (i + 1) % 2 (read during
+  // tile i + 1).
+  if (tile_lo < tile_hi) {
+    load_tile((uint32_t)(tile_lo * kKeys));
+    store_tile(0);
+    if (tile_lo + 1 < tile_hi) load_tile((uint32_t)((tile_lo + 1) * kKeys));
+  }
+  __syncthreads();
   for (int tile = tile_lo; tile < tile_hi; ++tile) {
     const int t0 = tile * kKeys;
-    __syncthreads();  // every wave is done reading the previous tile
-    store_tile();
-    if (tile + 1 < tile_hi) load_tile((uint32_t)(t0 + kKeys));
-    __syncthreads();
+    const int cur = (tile - tile_lo) & 1;
+    const uint16_t* kt = k_lds[cur];
+    const uint16_t* vt = v_lds[cur];
 
     // ---- S^T = K Q^T, 4 blocks of 16 keys (block kb, row i: key
     //      32 (kb / 2) + 8 (i / 4) + 4 (kb % 2) + i % 4) ----
@@ -302,10 +314,15 @@ void prefill_attn_kernel(const PrefillArgs a) {
       for (int r = 0; r < RB; ++r) st[r][kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
-        const uint4 ka = *(const uint4*)(k_lds + krow * KP + 32 * kk + 8 * lg);
+        const uint4 ka = *(const uint4*)(kt + krow * KP + 32 * kk + 8 * lg);
 #pragma unroll
         for (int r = 0; r < RB; ++r) st[r][kb] = mfma32<F16>(ka, qf[r][kk], st[r][kb]);
       }
+    }
+    // the next tile into the other buffer while the products run
+    if (tile + 1 < tile_hi) {
+      store_tile(cur ^ 1);
+      if (tile + 2 < tile_hi) load_tile((uint32_t)(t0 + 2 * kKeys));
     }
     // ---- online softmax (base 2) per query row; register j of block kb is
     //      key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j ----
@@ -348,13 +365,14 @@ void prefill_attn_kernel(const PrefillArgs a) {
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const uint4 va = *(const uint4*)(v_lds + (16 * nb + lq) * VP + 32 * h + 8 * lg);
+        const uint4 va = *(const uint4*)(vt + (16 * nb + lq) * VP + 32 * h + 8 * lg);
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
           const uint4 pb = make_uint4(pf[r][2 * h].x, pf[r][2 * h].y, pf[r][2 * h + 1].x, pf[r][2 * h + 1].y);
           o[r][nb] = mfma32<F16>(va, pb, o[r][nb]);
         }
       }
+    __syncthreads();
   }
 
   // ---- normalise and store: lane (lq, lg) holds dims 16 nb + 4 lg .. + 3 ----
