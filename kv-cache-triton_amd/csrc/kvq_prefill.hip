@@ -46,6 +46,11 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 constexpr int kRows = 64;    // query rows per workgroup (4 waves x 16)
 constexpr int kKeys = 64;    // keys per tile
 constexpr float kNegP = -1.0e30f;
+// Running-max slack (log2 units): a row's reference max moves, and its state
+// is rescaled, only when a tile's max exceeds it by more than this, so
+// weights 2^(s - m) stay below 2^8, which the fp16/bf16 weights and fp32 sums
+// hold with their full precision.
+constexpr float kLazyMaxP = 8.0f;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -327,10 +332,12 @@ void prefill_attn_kernel(const PrefillArgs a) {
     // ---- online softmax (base 2) per query row; register j of block kb is
     //      key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j ----
     uint2 pf[RB][4];
+    float mt[RB];
+    bool grow = false;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const bool full = t0 + kKeys <= lim[r];  // no key of this tile is masked for this row
-      float mt = kNegP;
+      mt[r] = kNegP;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -338,22 +345,34 @@ void prefill_attn_kernel(const PrefillArgs a) {
           float x = st[r][kb][j] * a.scale_log2;
           if (!full) x = t0 + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1) + j < lim[r] ? x : kNegP;
           st[r][kb][j] = x;
-          mt = fmaxf(mt, x);
+          mt[r] = fmaxf(mt[r], x);
         }
-      mt = fmaxf(mt, __shfl_xor(mt, 16));
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run[r], mt);
-      const float alpha = __builtin_amdgcn_exp2f(m_run[r] - m_new);
-      m_run[r] = m_new;
-      l_run[r] *= alpha;
+      mt[r] = fmaxf(mt[r], __shfl_xor(mt[r], 16));
+      mt[r] = fmaxf(mt[r], __shfl_xor(mt[r], 32));
+      grow = grow || mt[r] > m_run[r] + kLazyMaxP;
+    }
+    // lazy running max: the state is rescaled only in tiles where some row
+    // of the wave outgrows its reference by more than kLazyMaxP (wave-uniform)
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) o[r][nb] *= alpha;
+      for (int r = 0; r < RB; ++r) {
+        const float m_new = fmaxf(m_run[r], mt[r]);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[r] - m_new);
+        m_run[r] = m_new;
+        l_run[r] *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) o[r][nb] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const bool full = t0 + kKeys <= lim[r];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         float p[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(st[r][kb][j] - m_new);
+          p[j] = __builtin_amdgcn_exp2f(st[r][kb][j] - m_run[r]);
           if (!full) p[j] = st[r][kb][j] > kNegP ? p[j] : 0.0f;
           l_run[r] += p[j];
         }
