@@ -181,7 +181,8 @@ int kvq_decode_attn(const void* q, int q_dtype, const int64_t* q_strides,
  * (device int32 [B]) or pos0 for every sequence; its new row is written at
  * that index and it attends old length + 1 keys. A sequence whose old length
  * is not below `capacity` is left unchanged and attends its first `capacity`
- * keys (pos0 is checked on the host).
+ * keys; one whose old length is negative is left unchanged and yields zeros
+ * (pos0 is checked on the host).
  * group_size in {32, 64, 128}; D in {64, 128}. n_split / workspace as for
  * kvq_decode_attn (plan with s_max = the longest attended length).
  */

@@ -764,10 +764,11 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
     }
   }
 
+  const bool len_ok = L >= 0;  // a negative length: no keys, and no row written
   L = L < 0 ? 0 : L;
   // decode step: the new token goes to row L (if it fits the cache) and is
   // attended by the unit's last split from registers
-  bool has_new = a.append && L < a.Sk && split == a.n_split - 1;
+  bool has_new = a.append && len_ok && L < a.Sk && split == a.n_split - 1;
   L = L < a.Sk ? L : a.Sk;
   // The new token's rows (lane l: elements 2l, 2l+1): the K row for the
   // split's last wave, which quantizes, stores and scores it, the V row for
@@ -1461,13 +1462,14 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
 
   int L = !ROWMASK && a.append ? a.pos0 : a.Sk;
   if (a.seq_lens) L = a.seq_lens[b];
+  const bool len_ok = L >= 0;  // a negative length: no keys, and no row written
   L = L < 0 ? 0 : L;
   // decode step: the new token goes to row L (if it fits the cache) and is
   // attended by the unit's last split: wave 3 quantizes, stores and scores
   // its K row, wave 2 quantizes and stores its V row (lane l: elements 2l,
   // 2l+1, loaded here, ahead of the tiles). A decode step has one query
   // position, so it never takes the row-masked instances.
-  const bool has_new = !ROWMASK && a.append && L < a.Sk && split == a.n_split - 1;
+  const bool has_new = !ROWMASK && a.append && len_ok && L < a.Sk && split == a.n_split - 1;
   L = L < a.Sk ? L : a.Sk;
   float nx0 = 0.0f, nx1 = 0.0f;
   if (has_new && wave >= 2 && lane < D / 2) {

@@ -422,3 +422,30 @@ def test_decode_step_random_shapes(seed):
             ref[1][i:i + 1, :, :n].float().cpu().numpy(), ref[2][i:i + 1, :, :n].cpu().numpy(),
             ref[3][i:i + 1, :, :n].float().cpu().numpy(), group_size=G, scale=sm)
         assert np.abs(g[i:i + 1] - exact).max() <= tol, (i, np.abs(g[i:i + 1] - exact).max())
+
+
+@pytest.mark.parametrize("xdt,sdt", [("bf16", "bf16"), ("f32", "f32")])
+def test_decode_step_negative_position_writes_nothing(xdt, sdt):
+    """A negative old length (invalid input from a caller's device state)
+    leaves that sequence's cache untouched and yields zeros; the other
+    sequences step as usual. Both kernels."""
+    print(f"decode step with a negative position: {xdt}/{sdt}", flush=True)
+    B, Hq, Hkv, D, G, cap = 2, 8, 2, 128, 32, 300
+    b = _cache_dt(B, Hkv, cap, D, G, xdt, sdt, 200, seed=31)
+    before = [t.clone() for t in b]
+    q, kn, vn = _new_dt(B, Hq, Hkv, D, xdt, seed=31)
+    sm = D ** -0.5
+    pos = torch.tensor([-3, 150], dtype=torch.int32, device=DEV)
+    got = ops.decode_step(q, kn, vn, *b, pos, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    torch.cuda.synchronize()
+    for x, y in zip(b, before):
+        assert torch.equal(x[0], y[0])  # sequence 0 untouched
+    assert torch.all(got[0] == 0)
+    ref = [t[1:].clone() for t in before]
+    ops.quantize_into(kn[1:], ref[0], ref[1], G, 150)
+    ops.quantize_into(vn[1:], ref[2], ref[3], G, 150)
+    for x, y in zip(b, ref):
+        assert torch.equal(x[1:], y)
+    want = ops.fused_decode_attention(q[1:], *(t[:, :, :151] for t in ref), n_kv_heads=Hkv, group_size=G,
+                                      is_causal=False, sm_scale=sm)
+    _close_dt(got[1:], want, xdt)
