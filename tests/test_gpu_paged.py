@@ -474,3 +474,38 @@ def test_paged_random_shapes(seed):
                                         seq_lens=sl + 1)
     g_np, w_np = got_s.float().cpu().numpy(), want_s.float().cpu().numpy()
     assert np.all(np.abs(g_np - w_np) <= 2.0 ** -6 + 2.0 ** -7 * np.abs(w_np)), np.abs(g_np - w_np).max()
+
+
+def test_paged_cache_fp32_matches_contiguous_cache():
+    """fp32 activations (GPT-2-style exact path) in the paged cache: ragged
+    sequences, three decode steps, each within 1e-4 of the contiguous cache's
+    fused fp32 step and of the float64 oracle."""
+    print("paged cache, fp32 activations", flush=True)
+    B, Hq, Hkv, D, G = 3, 12, 12, 64, 32
+    g = torch.Generator().manual_seed(6)
+    k0 = torch.randn(B, Hkv, 400, D, generator=g).to(DEV)
+    v0 = torch.randn(B, Hkv, 400, D, generator=g).to(DEV)
+    lens = torch.tensor([400, 90, 257], dtype=torch.int32)
+    pc = PagedQuantizedKVCache(group_size=G, page_size=64)
+    pc.load_ragged(k0, v0, 0, lens)
+    cc = QuantizedKVCache(group_size=G)
+    cc.load_ragged(k0, v0, 0, lens)
+    sm = D ** -0.5
+    for step in range(3):
+        q = torch.randn(B, Hq, 1, D, generator=g).to(DEV)
+        kn = torch.randn(B, Hkv, 1, D, generator=g).to(DEV)
+        vn = torch.randn(B, Hkv, 1, D, generator=g).to(DEV)
+        got = pc.append_and_attend(q, kn, vn, 0, n_kv_heads=Hkv, scale=sm)
+        if got is None:  # the caller's route when the fused step does not apply
+            pc.append(kn, vn, 0)
+            got = pc.attend(q, 0, n_kv_heads=Hkv, scale=sm, is_causal=False)
+        want = cc.append_and_attend(q, kn, vn, 0, n_kv_heads=Hkv, scale=sm)
+        assert want is not None
+        g_np, w_np = got.cpu().numpy(), want.cpu().numpy()
+        assert np.abs(g_np - w_np).max() <= 1e-4
+        parts = [t.cpu() for t in pc.get_quantized(0)]
+        exact = O.attention_over_quantized(q.cpu().numpy(), parts[0].numpy(), parts[1].numpy(), parts[2].numpy(),
+                                           parts[3].numpy(), group_size=G, scale=sm,
+                                           seq_lens=pc.get_seq_lens(0).tolist())
+        assert np.abs(g_np - exact).max() <= 1e-4
+    assert pc.get_seq_lens(0).tolist() == [403, 93, 260]
