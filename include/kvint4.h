@@ -285,8 +285,9 @@ int kvq_prefill_attn(const void* q, int q_dtype, const int64_t* q_strides,
  *           length must not reach such a page).
  *
  * The attention entry points (kvq_decode_attn_paged, kvq_decode_step_paged)
- * need bf16/fp16 queries, 16-bit scales and page_size >= 64; a head's pool
- * must stay below 2 GiB. Planning and workspace: kvq_decode_attn_num_splits
+ * need page_size >= 64 (bf16/fp16 queries with 16-bit scales run on the
+ * matrix cores, fp32 queries or scales on the exact-fp32 kernel); a head's
+ * pool must stay below 2 GiB. Planning and workspace: kvq_decode_attn_num_splits
  * (s_max = the longest attended length) and kvq_decode_attn_workspace_bytes,
  * as for the contiguous cache.
  */

@@ -1433,7 +1433,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
 // Lane = token * (D/32) + chunk for QK (quad-reduced with DPP); V lanes own 8
 // output dims and four tokens per tile.
 
-template <int D, int ROWS, int QM, bool ROWMASK>
+template <int D, int ROWS, int QM, bool ROWMASK, bool PAGED>
 __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a) {
   constexpr int LPT = D / 32;
   constexpr int TPT = 64 / LPT;
@@ -1469,7 +1469,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   // its K row, wave 2 quantizes and stores its V row (lane l: elements 2l,
   // 2l+1, loaded here, ahead of the tiles). A decode step has one query
   // position, so it never takes the row-masked instances.
-  const bool has_new = !ROWMASK && a.append && len_ok && L < a.Sk && split == a.n_split - 1;
+  bool has_new = !ROWMASK && a.append && len_ok && L < a.Sk && split == a.n_split - 1;
   L = L < a.Sk ? L : a.Sk;
   float nx0 = 0.0f, nx1 = 0.0f;
   if (has_new && wave >= 2 && lane < D / 2) {
@@ -1486,9 +1486,25 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
       nx1 = QM == KVQ_F16 ? f16_bits_to_f32(x >> 16) : bf16_bits_to_f32(x >> 16);
     }
   }
+  // Paged caches: split boundaries at multiples of 64 keys, so that a tile
+  // of TPT (<= 64, dividing 64) keys lies inside one page and one table
+  // entry gives its pool rows; a pool with no block has nothing to read.
   int t_begin, t_end;
-  split_range(a, L, split, t_begin, t_end);
-  const int ntiles = t_end > t_begin ? (t_end - t_begin + TPT - 1) / TPT : 0;
+  if constexpr (PAGED) split_range64(a, L, split, t_begin, t_end);
+  else split_range(a, L, split, t_begin, t_end);
+  int ntiles = t_end > t_begin ? (t_end - t_begin + TPT - 1) / TPT : 0;
+  const int32_t* bt_b = PAGED ? a.bt + (int64_t)b * a.bt_stride : nullptr;
+  int64_t new_row = L;  // the new token's cache row (paged: its pool row)
+  if constexpr (PAGED) {
+    if (a.n_blocks == 0) ntiles = 0;
+    if (has_new) {
+      uint32_t dl;
+      bool ok;
+      page_delta(a, bt_b, (uint32_t)L, dl, ok);
+      has_new = ok;
+      new_row = (int64_t)(uint32_t)((uint32_t)L + dl);
+    }
+  }
 
   const int kt = lane / LPT;
   const int kc = lane % LPT;
@@ -1592,8 +1608,8 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     c0 = fminf(fmaxf(c0, -8.0f), 7.0f);
     c1 = fminf(fmaxf(c1, -8.0f), 7.0f);
     const uint32_t byte = (uint32_t)((int)c0 + 8) | ((uint32_t)((int)c1 + 8) << 4);
-    uint8_t* prow = const_cast<uint8_t*>(is_k ? kp_bh : vp_bh) + (int64_t)L * (is_k ? kps : vps);
-    char* srow = const_cast<char*>(is_k ? ks_bh : vs_bh) + (int64_t)L * (is_k ? kss : vss) * s_esize;
+    uint8_t* prow = const_cast<uint8_t*>(is_k ? kp_bh : vp_bh) + new_row * (is_k ? kps : vps);
+    char* srow = const_cast<char*>(is_k ? ks_bh : vs_bh) + new_row * (is_k ? kss : vss) * s_esize;
     if (byte_ok) prow[lane] = (uint8_t)byte;
     float sq = scale;
     const bool scale_lane = byte_ok && (2 * lane) % G == 0;
@@ -1637,17 +1653,27 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
     uint4 kcode[CH];
     uint32_t vcode[CH][4];
     float sk[CH], sv[CH];
+    bool blk_ok[CH];  // paged: a block holds the tile's page (else its rows read pool row 0, masked)
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       if (i >= nv) break;
       const int t0 = t_begin + (base + 4 * i) * TPT;
-      const uint32_t tk = (uint32_t)min(t0 + kt, last_tok);
+      // token -> cache row: the token itself, or (paged) its pool row; the
+      // clamp to the last token stays inside the tile, hence inside its page
+      uint32_t dl = 0u;
+      blk_ok[i] = true;
+      if constexpr (PAGED) page_delta(a, bt_b, (uint32_t)t0, dl, blk_ok[i]);
+      auto row = [&](int t) -> uint32_t {
+        const uint32_t tc = (uint32_t)min(t, last_tok);
+        return blk_ok[i] ? tc + dl : 0u;
+      };
+      const uint32_t tk = row(t0 + kt);
       kcode[i] = *(const uint4*)(kp_bh + (tk * kps + 16u * kc));
       sk[i] = load_scale(ks_bh, tk * kss + gK, a.scale_dtype);
       sv[i] = load_scale(vs_bh, tk * vss + gK, a.scale_dtype);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint32_t tv = (uint32_t)min(t0 + vts + VTS * k, last_tok);
+        const uint32_t tv = row(t0 + vts + VTS * k);
         vcode[i][k] = *(const uint32_t*)(vp_bh + (tv * vps + 4u * vj));
       }
     }
@@ -1661,7 +1687,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
         continue;
       }
       const int t = t_begin + (base + 4 * i) * TPT + kt;
-      const bool tv_ok = (base + 4 * i < ntiles) && (t < t_end);
+      const bool tv_ok = (base + 4 * i < ntiles) && (t < t_end) && blk_ok[i];
       float acc[ROWS];
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) acc[r] = qinit[r];
@@ -1930,8 +1956,13 @@ static void launch_mfma(const AttnArgs& a, int rows, bool rowmask, dim3 grid, hi
 
 template <int D, int ROWS, int QM>
 static void launch_valu_rows(const AttnArgs& a, bool rowmask, dim3 grid, hipStream_t st) {
-  if (rowmask) hipLaunchKernelGGL((decode_attn_valu_kernel<D, ROWS, QM, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((decode_attn_valu_kernel<D, ROWS, QM, false>), grid, dim3(256), 0, st, a);
+  if (a.bt) {
+    if (rowmask) hipLaunchKernelGGL((decode_attn_valu_kernel<D, ROWS, QM, true, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_attn_valu_kernel<D, ROWS, QM, false, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (rowmask) hipLaunchKernelGGL((decode_attn_valu_kernel<D, ROWS, QM, true, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_attn_valu_kernel<D, ROWS, QM, false, false>), grid, dim3(256), 0, st, a);
+  }
 }
 
 template <int D, int QM>
@@ -2106,11 +2137,6 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
                       pg->bt_cols < (1ll << 31) && pg->bt_stride >= pg->bt_cols,
                   "kvq_decode_attn_paged: bad block table geometry");
     KVQ_CHECK_ARG(pg->bt != nullptr || pg->bt_cols == 0, "kvq_decode_attn_paged: null block table");
-    if (!mfma) {
-      set_error("kvq_decode_attn_paged: paged caches take the matrix-core kernel (bf16/fp16 queries, "
-                "16-bit scales)");
-      return KVQ_EUNSUP;
-    }
   }
   KVQ_CHECK_ARG(Sk * kMaxSplit < (1ll << 32) && Sq <= 0x7fffffffll, "kvq_decode_attn: sequence too long");
 

@@ -805,9 +805,10 @@ def fused_decode_attention_paged(
     n_split: int | None = None,
 ) -> torch.Tensor:
     """fused_decode_attention over a paged cache. Sequence b attends its first
-    seq_lens[b] tokens (device int32 [B]) or `seq_len` tokens. Raises
-    KVQUnsupported where the kernel does not apply (fp32 queries or scales,
-    page_size < 64)."""
+    seq_lens[b] tokens (device int32 [B]) or `seq_len` tokens. bf16/fp16
+    queries with 16-bit scales run on the matrix cores, fp32 queries or scales
+    on the exact-fp32 kernel. Raises KVQUnsupported where neither applies
+    (page_size < 64)."""
     _check_cuda(q, k_pool, k_scales, v_pool, v_scales, pt.table, what="fused_decode_attention_paged")
     B, Hq, Sq, D = q.shape
     if pt.table.shape[0] < B:

@@ -478,8 +478,8 @@ def test_paged_random_shapes(seed):
 
 def test_paged_cache_fp32_matches_contiguous_cache():
     """fp32 activations (GPT-2-style exact path) in the paged cache: ragged
-    sequences, three decode steps, each within 1e-4 of the contiguous cache's
-    fused fp32 step and of the float64 oracle."""
+    sequences, three fused decode steps, each within 1e-4 of the contiguous
+    cache's fused fp32 step and of the float64 oracle."""
     print("paged cache, fp32 activations", flush=True)
     B, Hq, Hkv, D, G = 3, 12, 12, 64, 32
     g = torch.Generator().manual_seed(6)
@@ -496,9 +496,7 @@ def test_paged_cache_fp32_matches_contiguous_cache():
         kn = torch.randn(B, Hkv, 1, D, generator=g).to(DEV)
         vn = torch.randn(B, Hkv, 1, D, generator=g).to(DEV)
         got = pc.append_and_attend(q, kn, vn, 0, n_kv_heads=Hkv, scale=sm)
-        if got is None:  # the caller's route when the fused step does not apply
-            pc.append(kn, vn, 0)
-            got = pc.attend(q, 0, n_kv_heads=Hkv, scale=sm, is_causal=False)
+        assert got is not None  # the paged fp32 decode step (one launch)
         want = cc.append_and_attend(q, kn, vn, 0, n_kv_heads=Hkv, scale=sm)
         assert want is not None
         g_np, w_np = got.cpu().numpy(), want.cpu().numpy()
@@ -509,3 +507,68 @@ def test_paged_cache_fp32_matches_contiguous_cache():
                                            seq_lens=pc.get_seq_lens(0).tolist())
         assert np.abs(g_np - exact).max() <= 1e-4
     assert pc.get_seq_lens(0).tolist() == [403, 93, 260]
+
+
+
+TDT32 = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+@pytest.mark.parametrize("xdt,sdt,B,Hq,Hkv,D,G,P,lens", [
+    ("f32", "f32", 2, 12, 12, 64, 32, 64, [1000, 130]),
+    ("f32", "f16", 3, 32, 8, 128, 64, 128, [700, 1, 2049]),
+    ("bf16", "f32", 2, 16, 4, 128, 32, 64, [333, 900]),
+    ("f32", "bf16", 1, 8, 2, 64, 128, 256, [600]),
+])
+def test_fp32_kernel_paged_matches_contiguous(xdt, sdt, B, Hq, Hkv, D, G, P, lens):
+    """The exact-fp32 kernel over a paged cache (fp32 queries or fp32
+    scales): at one split bit-identical to the contiguous kernel over the
+    gathered rows, at the planner's splits within its bar of the oracle; the
+    paged decode step writes the quantizer's bytes through the table and
+    matches the contiguous step."""
+    print(f"fp32 kernel, paged: {xdt}/{sdt} B {B} Hq {Hq} Hkv {Hkv} D {D} G {G} P {P} lens {lens}", flush=True)
+    t, st = TDT32[xdt], TDT32[sdt]
+    n_blocks = sum(-(-(n + 1) // P) for n in lens) + 2
+    table = _table([n + 1 for n in lens], P, n_blocks, seed=P + len(lens))
+    pt = ops.PageTable(table, P, n_blocks)
+    pools = _pools(Hkv, n_blocks, P, D, G, st)
+    S = max(lens)
+    g = torch.Generator().manual_seed(S + D)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(t)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(t)
+    ops.quantize_into_paged(k.to(DEV), pools[0], pools[1], pt, G, 0)
+    ops.quantize_into_paged(v.to(DEV), pools[2], pools[3], pt, G, 0)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(t).to(DEV)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    sm = D ** -0.5
+    cont = [_gather(p, table, P, S).contiguous() for p in pools]
+    got1 = ops.fused_decode_attention_paged(q, *pools, pt, n_kv_heads=Hkv, group_size=G, is_causal=False,
+                                            sm_scale=sm, seq_lens=sl, n_split=1)
+    want1 = ops.fused_decode_attention(q, *cont, n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm,
+                                       seq_lens=sl, n_split=1)
+    assert torch.equal(got1, want1)
+    got = ops.fused_decode_attention_paged(q, *pools, pt, n_kv_heads=Hkv, group_size=G, is_causal=False,
+                                           sm_scale=sm, seq_lens=sl)
+    exact = O.attention_over_quantized(q.float().cpu().numpy(), *(c.cpu().numpy() if c.dtype == torch.uint8
+                                       else c.float().cpu().numpy() for c in cont),
+                                       group_size=G, scale=sm, seq_lens=lens)
+    tol = 1e-4 if xdt == "f32" else 2e-2
+    assert np.abs(got.float().cpu().numpy() - exact).max() <= tol
+    # the paged decode step
+    kn = (3 * torch.randn(B, Hkv, 1, D, generator=g)).to(t).to(DEV)
+    vn = torch.randn(B, Hkv, 1, D, generator=g).to(t).to(DEV)
+    got_s = ops.decode_step_paged(q, kn, vn, *pools, pt, sl, n_kv_heads=Hkv, group_size=G, sm_scale=sm)
+    want_kp, want_ks = O.quantize_int4(kn.float().cpu().numpy(), G, sdt)
+    want_vp, want_vs = O.quantize_int4(vn.float().cpu().numpy(), G, sdt)
+    cont = [_gather(p, table, P, S + 1).contiguous() for p in pools]
+    for b, n in enumerate(lens):
+        assert np.array_equal(cont[0][b, :, n].cpu().numpy(), want_kp[b, :, 0])
+        assert np.array_equal(cont[2][b, :, n].cpu().numpy(), want_vp[b, :, 0])
+        assert np.array_equal(O.bits(cont[1][b, :, n].float().cpu().numpy(), sdt), O.bits(want_ks[b, :, 0], sdt))
+        assert np.array_equal(O.bits(cont[3][b, :, n].float().cpu().numpy(), sdt), O.bits(want_vs[b, :, 0], sdt))
+    want_s = ops.fused_decode_attention(q, *cont, n_kv_heads=Hkv, group_size=G, is_causal=False, sm_scale=sm,
+                                        seq_lens=sl + 1)
+    g_np, w_np = got_s.float().cpu().numpy(), want_s.float().cpu().numpy()
+    if xdt == "f32":
+        assert np.abs(g_np - w_np).max() <= 1e-4 + 1e-4 * np.abs(w_np).max()
+    else:
+        assert np.all(np.abs(g_np - w_np) <= 2.0 ** -6 + 2.0 ** -7 * np.abs(w_np)), np.abs(g_np - w_np).max()
