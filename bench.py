@@ -14,8 +14,10 @@ Default workload "ns": Llama-3.1-8B attention shape (32 query heads, 8 KV
 heads, head dim 128, group 32, bf16) at 16K context, 32 layers. Printed: one
 JSON line with whole-job algorithmic GB/s (`value`), ms per token, the
 attention kernel's roofline (algorithmic bytes / average launch time from HIP
-events around every launch, vs 8 TB/s), and the CPU baseline (the C
-restatement of the reference's CPU path, timed on a bounded sample).
+events around every launch, vs 8 TB/s; the counter-measured HBM bytes of the
+committed rocprof summary over the same time as traffic_gbs), and the CPU
+baseline (the reference's PyTorch CPU path restated in torch, with the C
+restatement beside it, each timed on a bounded sample).
 """
 
 from __future__ import annotations
@@ -339,6 +341,11 @@ def main() -> int:
             "bytes_per_launch": k_bytes,
         },
     }
+    traffic = result["roofline"]["traffic"]
+    if traffic:
+        # HBM bytes the counters saw per launch (FETCH_SIZE + WRITE_SIZE, from the
+        # committed summary) over this run's launch time
+        result["roofline"]["traffic_gbs"] = round(traffic / (attn_us * 1e-6) / 1e9, 2)
 
     if not args.no_ceiling and P == 0:
         # the same bytes read by a kernel that does nothing else (one buffer
