@@ -826,10 +826,15 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // ---- cache slices as bounds-checked buffers (contiguous: rows >= t_end
   //      read as zero; paged: the KV head's pool, rows addressed through the
   //      block table, tokens >= t_end given an out-of-range offset) ----
-  const uint8_t* kp_bh = a.kp + (int64_t)b * a.kps_b + (int64_t)kvh * a.kps_h;
-  const uint8_t* vp_bh = a.vp + (int64_t)b * a.vps_b + (int64_t)kvh * a.vps_h;
-  const uint16_t* ks_bh = (const uint16_t*)a.ks + ((int64_t)b * a.kss_b + (int64_t)kvh * a.kss_h);
-  const uint16_t* vs_bh = (const uint16_t*)a.vs + ((int64_t)b * a.vss_b + (int64_t)kvh * a.vss_h);
+  // (b, kvh) slice offsets: head strides are below 2^32 (host), so the head
+  // term is one 32 x 32 -> 64-bit product; b and kvh are non-negative
+  auto slice_off = [&](int64_t sb, int64_t sh) -> uint64_t {
+    return (uint64_t)(uint32_t)b * (uint64_t)sb + (uint64_t)(uint32_t)kvh * (uint32_t)sh;
+  };
+  const uint8_t* kp_bh = a.kp + slice_off(a.kps_b, a.kps_h);
+  const uint8_t* vp_bh = a.vp + slice_off(a.vps_b, a.vps_h);
+  const uint16_t* ks_bh = (const uint16_t*)a.ks + slice_off(a.kss_b, a.kss_h);
+  const uint16_t* vs_bh = (const uint16_t*)a.vs + slice_off(a.vss_b, a.vss_h);
   const uint32_t kps = (uint32_t)a.kps_s, vps = (uint32_t)a.vps_s;
   const uint32_t kss2 = 2u * (uint32_t)a.kss_s, vss2 = 2u * (uint32_t)a.vss_s;
   const uint32_t Le = PAGED ? a.pool_rows : (uint32_t)t_end;
@@ -1135,7 +1140,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       permlane32_swap(u, v);
       am = fmax_nc(u, v);
     }
-    const float scale = am > 0.0f ? am / 7.0f : 1.0f;
+    const float scale = group_scale(am);  // am / 7, correctly rounded
     const float inv = 1.0f / scale;
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
     float c0 = rint_quotient(x0, scale, inv, fast), c1 = rint_quotient(x1, scale, inv, fast);
@@ -1146,7 +1151,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
     uint8_t* prow = const_cast<uint8_t*>(is_k ? kp_bh : vp_bh) + new_row * (is_k ? kps : vps);
     uint16_t* srow = const_cast<uint16_t*>(is_k ? ks_bh : vs_bh) + new_row * (is_k ? a.kss_s : a.vss_s);
     if (byte_ok) prow[lane] = (uint8_t)byte;
-    if (byte_ok && (2 * lane) % G == 0) srow[(2 * lane) / G] = (uint16_t)sbits;
+    if (byte_ok && ((2 * lane) & (G - 1)) == 0) srow[(2 * lane) / G] = (uint16_t)sbits;  // G: 32, 64 or 128
     const float sq = scale16_to_f32(sbits, S_F16);
     const float d0 = c0 * sq, d1 = c1 * sq;
     if (is_k) {
@@ -1390,7 +1395,14 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   float lsum[RS][4];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) wave_reduce4<true>(l_acc[rs], lsum[rs]);
-  __syncthreads();
+  // o_lds[wave] occupies exactly the bytes of w_lds[wave] (RS * 16 * D of
+  // them in both layouts), so only this wave's own weight reads must be done
+  // before they are overwritten: a wave-level ordering point, no workgroup
+  // barrier.
+  static_assert(sizeof(float) * ROWS * D == 2 * RS * 4 * LPT * NSUB * VTS * 4, "o_lds[w] aliases w_lds[w] exactly");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
   for (int i = 0; i < NK; i += 4) {
     const int idx = NK * vts + i;  // first of 4 consecutive values (same row)
@@ -1601,7 +1613,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
       permlane32_swap(u, v);
       am = fmax_nc(u, v);
     }
-    const float scale = am > 0.0f ? am / 7.0f : 1.0f;
+    const float scale = group_scale(am);  // am / 7, correctly rounded
     const float inv = 1.0f / scale;
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
     float c0 = rint_quotient(x0, scale, inv, fast), c1 = rint_quotient(x1, scale, inv, fast);
@@ -2119,6 +2131,14 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
     s_al = s_al && (uintptr_t)k_scales % sz == 0 && (uintptr_t)v_scales % sz == 0;
     if (!s_al) {
       set_error("kvq_decode_attn: scale rows must be %lld-byte aligned", (long long)sz);
+      return KVQ_EUNSUP;
+    }
+  }
+  // Cache strides are non-negative and head strides below 2^32 (the kernels
+  // form the head term of a slice offset as a 32 x 32 -> 64-bit product).
+  for (const int64_t* st : {kp_strides, ks_strides, vp_strides, vs_strides}) {
+    if (st[0] < 0 || st[1] < 0 || st[1] >= (1ll << 32)) {
+      set_error("kvq_decode_attn: cache strides must be non-negative and head strides below 2^32");
       return KVQ_EUNSUP;
     }
   }

@@ -29,6 +29,22 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// The group scale absmax / 7 as the IEEE (correctly rounded) fp32 quotient,
+// or 1 for an all-zero group (the reference's rule,
+// kernels/llama3/quantize.py:137-141), without a division: q = am * RN(1/7)
+// corrected once with an fma, q1 = q + (am - 7 q) * RN(1/7). q1 equals the
+// quotient bit for bit for every non-negative finite am (checked exhaustively
+// by oracle/kvq_ref.c kvq_ref_check_div7, a CPU test). An infinite absmax
+// keeps q (infinity, like the division); NaN yields 1, as the comparison
+// with zero does in the reference.
+__device__ __forceinline__ float group_scale(float am) {
+  constexpr float kInv7 = 1.0f / 7.0f;
+  const float q = am * kInv7;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q, 7.0f, am), kInv7, q);
+  const float s = q1 == q1 ? q1 : q;
+  return am > 0.0f ? s : 1.0f;
+}
+
 // rint(x / s) where x / s is the IEEE (correctly rounded) fp32 quotient, for
 // |x| <= 7 s (x an element of the group whose absmax / 7 is s, s normal):
 // t = x * (1 / s), both steps correctly rounded, lies within 2^-19.6 of the

@@ -68,8 +68,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
 
   float amax = 0.0f;
   for (int64_t c = c0; c < c1; ++c) amax = fmaxf(amax, fabsf(ld_x<XDT>(a.x, xbase + c * a.xs_d)));
-  // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
-  const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+  const float scale = group_scale(amax);  // amax / 7, correctly rounded
 
   const int64_t pos = dest_row(a, b, (a.write_pos ? (int64_t)a.write_pos[b] : a.write_pos0) + s);
   if (pos < 0) return;  // no destination row: past the capacity, or no block holds it
@@ -208,8 +207,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     if constexpr (LPG >= 8) amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
     if constexpr (LPG >= 16) amax = fmaxf(amax, dpp_f<0x140>(amax)); // row_mirror
     if (!live[k]) continue;
-    // IEEE-754 fp32 division, correctly rounded (hipcc's default for '/').
-    const float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+    const float scale = group_scale(amax);  // amax / 7, correctly rounded
     const float inv = 1.0f / scale;
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
     uint32_t word = 0;

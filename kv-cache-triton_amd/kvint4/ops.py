@@ -628,11 +628,14 @@ def attention_over_quantized(
     sm_scale: float,
     seq_lens: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Route by query rows per KV head: the fused decode kernel for short
-    blocks (decode, speculative blocks), the matrix-core prefill kernel for
-    long blocks after cached tokens (prompt chunks; one length for the
-    batch), and dequantize + dense SDPA for whole prompts and what neither
-    kernel takes."""
+    """Route by query rows per KV head: the matrix-core prefill kernel for
+    long blocks with one length for the batch (whole prompts and prompt
+    chunks, use_prefill_kernel), the fused decode kernel for blocks of at
+    most MAX_FUSED_ROWS rows (decode, speculative blocks) and for causal
+    blocks after cached tokens that the dense route would mask explicitly
+    (fp32 queries or per-sequence lengths), and dequantize + dense SDPA for
+    the rest (KVQ_EUNSUP shapes, long blocks the prefill kernel does not
+    take)."""
     B, Hq, Sq, D = q.shape
     Sk = k_packed.shape[2]
     rows = (Hq // n_kv_heads) * Sq

@@ -216,3 +216,30 @@ int kvqref_decode_attn(const float* q, const uint8_t* kp, const float* ks, const
   free(pm); free(pl); free(po);
   return 0;
 }
+
+/*
+ * Exhaustive check of the division-free group scale the HIP kernels use
+ * (kv-cache-triton_amd/csrc/kvq_common.h group_scale): for every
+ * non-negative finite fp32 value am with bit pattern in [lo, hi), the
+ * product q = am * RN(1/7) corrected once with a fused multiply-add,
+ * q + (am - 7 q) * RN(1/7), must equal the IEEE quotient am / 7 that the
+ * reference's torch path computes (kernels/llama3/quantize.py:137-141).
+ * Returns the number of bit patterns for which it does not ([0, 0x7f800000)
+ * covers zero, the subnormals and every normal value).
+ */
+int64_t kvqref_check_div7(uint32_t lo, uint32_t hi) {
+  const float inv7 = 1.0f / 7.0f;
+  int64_t bad = 0;
+  if (hi > 0x7f800000u) hi = 0x7f800000u;
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+  for (int64_t u = lo; u < (int64_t)hi; ++u) {
+    const uint32_t w = (uint32_t)u;
+    float am;
+    memcpy(&am, &w, 4);
+    const float q = am * inv7;
+    const float q1 = fmaf(fmaf(-q, 7.0f, am), inv7, q);
+    const float e = am / 7.0f;
+    if (memcmp(&q1, &e, 4) != 0) ++bad;
+  }
+  return bad;
+}

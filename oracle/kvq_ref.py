@@ -34,6 +34,8 @@ def lib() -> ctypes.CDLL:
         l.kvqref_decode_attn.restype = i32
         l.kvqref_num_threads.argtypes = []
         l.kvqref_num_threads.restype = i32
+        l.kvqref_check_div7.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+        l.kvqref_check_div7.restype = i64
         _lib = l
     return _lib
 

@@ -145,3 +145,13 @@ def test_c_matches_numpy_large():
         p2, s2 = R.quantize_int4(x, 32, dt)
         assert np.array_equal(p1, p2)
         assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
+def test_group_scale_without_division_is_exact():
+    """The HIP kernels form the group scale absmax / 7 without a division
+    (kv-cache-triton_amd/csrc/kvq_common.h group_scale: am * RN(1/7) corrected
+    once with an fma). Checked against the IEEE quotient the reference computes
+    (kernels/llama3/quantize.py:137-141) for every non-negative finite float:
+    zero, all subnormals and all normal values (oracle/kvq_ref.c
+    kvqref_check_div7)."""
+    assert R.lib().kvqref_check_div7(0, 0x7F800000) == 0
