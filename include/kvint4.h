@@ -44,7 +44,11 @@ enum kvq_status {
   KVQ_EUNSUP = -4    /* shape valid but not handled by the fused kernel */
 };
 
-/* Library version: major*10000 + minor*100 + patch. */
+/* Library version: major*10000 + minor*100 + patch. kvq_version() returns
+ * the version the library was built as; a binding declares the argument lists
+ * of one major version and must refuse a library of another. 2.0.0 added the
+ * capacity argument of kvq_quantize (1.x had none). */
+#define KVQ_VERSION 20000
 int kvq_version(void);
 
 /* Thread-local message describing the last error on this thread ("" if none). */

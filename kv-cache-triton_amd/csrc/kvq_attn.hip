@@ -46,6 +46,7 @@
 // Softmax runs in base 2 with sm_scale*log2(e) folded into the key scale.
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 
@@ -79,7 +80,9 @@ constexpr int kPhaseSlots = 16;
 // Stamp points: 0 entry, 1 first tiles' loads issued, 2 first tile's keys
 // arrived, 3 its values arrived, 4 tile loop done, 5 workgroup fold done,
 // 6 partial stores acknowledged, 7 arrival counted (thread 0), 8 merge start,
-// 9 merge inputs arrived, 10 merged output computed, 11 exit.
+// 9 merge inputs arrived, 10 merged output computed, 11 exit. Slot 12 holds
+// the wave's XCC id (written with the entry stamp), not a time.
+constexpr int kXccSlot = 12;
 
 struct AttnArgs {
   const void* q;
@@ -139,7 +142,11 @@ __device__ __forceinline__ void phase_stamp(unsigned long long* p, int point) {
   asm volatile("" ::: "memory");
   if (p != nullptr && (threadIdx.x & 63) == 0) {
     const size_t wg = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z);
-    p[(wg * 16 + (threadIdx.x >> 6)) * kPhaseSlots + point] = t;
+    unsigned long long* slot = p + (wg * 16 + (threadIdx.x >> 6)) * kPhaseSlots;
+    slot[point] = t;
+    // at entry, also the XCD the wave runs on: HW_REG_XCC_ID (hwreg 20),
+    // bits [3:0]
+    if (point == 0) slot[kXccSlot] = __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11));
   }
 }
 #endif
@@ -2078,6 +2085,47 @@ struct PagedArgs {
   int64_t bt_stride, bt_cols, n_blocks, page_size;
 };
 
+// The cross-split merge relies on how gfx950 (MI355X) deals workgroups to its
+// XCDs: round-robin over the XCDs in launch order, 8 per device in SPX mode
+// (fewer in the partition modes, still a divisor of 8), so the splits of a unit
+// (equal x % 8, unit_and_split) share one XCD and its L2. The library is built
+// for gfx950 only; the device's architecture is still checked, once per device,
+// before a split plan runs, so a launch on another part is refused instead of
+// merging partials across L2s it does not keep coherent.
+static std::mutex g_arch_mu;
+static int8_t g_arch_ok[64] = {};  // 0 not checked, 1 gfx950, -1 another part
+
+static int split_merge_device_ok() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("kvq_decode_attn: hipGetDevice: %s", hipGetErrorString(e));
+    return KVQ_EHIP;
+  }
+  if (dev < 0 || dev >= 64) {
+    set_error("kvq_decode_attn: device %d beyond the 64 devices the split check tracks", dev);
+    return KVQ_EUNSUP;
+  }
+  std::lock_guard<std::mutex> lock(g_arch_mu);
+  if (g_arch_ok[dev] == 0) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) {
+      set_error("kvq_decode_attn: hipGetDeviceProperties(%d): %s", dev, hipGetErrorString(e));
+      return KVQ_EHIP;
+    }
+    g_arch_ok[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+                             (prop.gcnArchName[6] == '\0' || prop.gcnArchName[6] == ':')
+                         ? 1 : -1;
+  }
+  if (g_arch_ok[dev] < 0) {
+    set_error("kvq_decode_attn: split plans need a gfx950 device (MI355X); device %d is another part "
+              "(use n_split = 1)", dev);
+    return KVQ_EUNSUP;
+  }
+  return KVQ_OK;
+}
+
 static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides,
                                const void* k_packed, const int64_t* kp_strides,
                                const void* k_scales, const int64_t* ks_strides,
@@ -2171,6 +2219,10 @@ static int decode_attn_impl(const void* q, int q_dtype, const int64_t* q_strides
     set_error("kvq_decode_attn: workspace too small (%lld < %lld bytes)",
               (long long)workspace_bytes, (long long)need);
     return KVQ_ESPACE;
+  }
+  if (p.n_split > 1) {
+    const int drc = split_merge_device_ok();
+    if (drc != KVQ_OK) return drc;
   }
 
   AttnArgs a;

@@ -19,6 +19,6 @@ void clear_error() { g_err[0] = '\0'; }
 
 }  // namespace kvq
 
-extern "C" int kvq_version(void) { return 100; }
+extern "C" int kvq_version(void) { return KVQ_VERSION; }
 
 extern "C" const char* kvq_last_error(void) { return kvq::g_err; }

@@ -19,6 +19,11 @@ LIB_PATH = os.path.join(_HERE, "libkvint4.so")
 KVQ_BF16, KVQ_F16, KVQ_F32 = 0, 1, 2
 KVQ_OK, KVQ_EINVAL, KVQ_ESPACE, KVQ_EHIP, KVQ_EUNSUP = 0, -1, -2, -3, -4
 
+# The argument lists below are those of major version 2 (KVQ_VERSION in
+# include/kvint4.h: major*10000 + minor*100 + patch); a library of another
+# major version would take them in another order, so it is refused.
+KVQ_MAJOR = 2
+
 DTYPE_CODE = {torch.bfloat16: KVQ_BF16, torch.float16: KVQ_F16, torch.float32: KVQ_F32}
 
 # Every symbol include/kvint4.h declares (checked by the CPU test suite).
@@ -175,6 +180,12 @@ def lib() -> ctypes.CDLL:
                 )
             handle = ctypes.CDLL(LIB_PATH)
             _declare(handle)
+            version = int(handle.kvq_version())
+            if version // 10000 != KVQ_MAJOR:
+                raise RuntimeError(
+                    f"kvint4: {LIB_PATH} is version {version}, this binding needs major version "
+                    f"{KVQ_MAJOR}; rebuild it (python -m kvint4.build)"
+                )
             _lib = handle
     return _lib
 

@@ -29,7 +29,9 @@ SOURCES = ("kvq_capi.hip", "kvq_quant.hip", "kvq_attn.hip", "kvq_prefill.hip")
 # (176 copies) and runs four waves per SIMD instead of three.
 SOURCE_FLAGS = {"kvq_attn.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=true"),
                 "kvq_prefill.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=true")}
-ARCH = os.environ.get("KVQ_OFFLOAD_ARCH", "gfx950")
+# gfx950 only: the decode kernels assume its wave64 MFMA forms and its
+# round-robin workgroup-to-XCD dispatch (checked again at run time).
+ARCH = "gfx950"
 
 # Packed-FP32 VALU forms are kept out of the generated code (the value path is
 # written in scalar fp32 and v_dot2); -O3 and IEEE division are the defaults.

@@ -19,7 +19,8 @@ each, norm, LM head, argmax) is captured once into a HIP graph and replayed:
     under the graph, and two decoders share no arrival counters;
   * every replay first checks that the cache still has the buffers the graph
     was captured with (reorder, batch select, crop-and-regrow or a load
-    replace them) and raises otherwise.
+    replace them) and the lengths the previous steps left (a crop changes
+    them in place), and raises otherwise.
 
 Batches with padding are not supported: the step runs without an attention
 mask, so every sequence of the batch must hold the same number of tokens.
@@ -177,6 +178,13 @@ class GraphedGreedyDecoder:
         if self.cache.buffer_signature() != self._signature:
             raise RuntimeError("the cache's buffers changed since the decode step was captured (a reorder, "
                                "batch select, growth or load); capture a new GraphedGreedyDecoder")
+        # an in-place edit keeps the buffers but moves the lengths (a crop):
+        # the replay would append at the device positions of the uncropped
+        # cache while the host reports the cropped ones
+        want = {i: int(b) + (self.done - self._base_done) for i, b in self._base.items()}
+        if self.cache.host_lengths() != want:
+            raise RuntimeError("the cache's lengths changed since the last decode step (a crop, or tokens "
+                               "appended outside the decoder); capture a new GraphedGreedyDecoder")
         self.graph.replay()
         self.done += 1
         self.cache.advance_host_lengths(self._base, self.done - self._base_done)

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_error_slot():
     lib = nat.lib()
-    assert lib.kvq_version() >= 100
+    assert lib.kvq_version() // 10000 == nat.KVQ_MAJOR
     assert isinstance(nat.last_error(), str)
 
 

@@ -162,3 +162,19 @@ def test_decoder_rejects_what_it_cannot_capture():
         GraphedGreedyDecoder(model, cache, nxt, max_new_tokens=2, warmup_steps=2)
     with pytest.raises(ValueError):
         QuantizedKVCache(group_size=32).make_static(4)
+
+
+def test_crop_between_replays_stops_the_decoder():
+    """A crop keeps the cache's buffers and moves its lengths: the captured
+    step would append at the uncropped positions, so step() must refuse."""
+    model = _model(64)
+    prompt = torch.randint(0, 512, (1, 40), generator=torch.Generator().manual_seed(7)).to(DEV)
+    cache, _, nxt = _prefill(model, prompt)
+    dec = GraphedGreedyDecoder(model, cache, nxt, max_new_tokens=6, warmup_steps=1)
+    dec.step()
+    torch.cuda.synchronize()
+    n = cache.get_seq_length()
+    cache.crop(n - 1)
+    assert cache.get_seq_length() == n - 1
+    with pytest.raises(RuntimeError, match="lengths changed"):
+        dec.step()

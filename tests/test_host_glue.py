@@ -212,6 +212,58 @@ def test_graph_decoder_rejects_unswapped_models_and_other_caches():
     del PagedQuantizedKVCache
 
 
+def test_graph_decoder_replay_checks_buffers_and_lengths():
+    """step() replays only while the cache holds the captured buffers and the
+    lengths the previous replays left; a crop keeps the buffers but moves the
+    lengths and must stop the replay before it runs."""
+    from kvint4.llama3.graph_decode import GraphedGreedyDecoder
+
+    class Cache:
+        def __init__(self):
+            self.lengths = {0: 40, 1: 40}
+            self.sig = ("bufs",)
+
+        def buffer_signature(self):
+            return self.sig
+
+        def host_lengths(self):
+            return dict(self.lengths)
+
+        def advance_host_lengths(self, base, n):
+            self.lengths = {i: b + n for i, b in base.items()}
+
+        def crop(self, max_length):
+            self.lengths = {i: min(n, max_length) for i, n in self.lengths.items()}
+
+    class Graph:
+        replays = 0
+
+        def replay(self):
+            Graph.replays += 1
+
+    def decoder(cache):
+        d = object.__new__(GraphedGreedyDecoder)
+        d.cache, d.graph, d.max_new_tokens = cache, Graph(), 8
+        d.done, d._base_done, d._base = 1, 1, cache.host_lengths()
+        d._signature = cache.buffer_signature()
+        return d
+
+    c = Cache()
+    d = decoder(c)
+    d.step()
+    d.step()
+    assert Graph.replays == 2 and c.lengths == {0: 42, 1: 42} and d.done == 3
+    c.crop(41)
+    with pytest.raises(RuntimeError, match="lengths changed"):
+        d.step()
+    assert Graph.replays == 2 and d.done == 3
+    c.lengths = {0: 42, 1: 42}
+    c.sig = ("other bufs",)
+    with pytest.raises(RuntimeError, match="buffers changed"):
+        d.step()
+    assert Graph.replays == 2
+
+
 def test_paged_make_static_takes_blocks_unshares_them_and_fixes_the_table(monkeypatch):
     """PagedQuantizedKVCache.make_static (host bookkeeping, CPU pools; the
     table holder's device check is lifted for the test): the blocks for the
