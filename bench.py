@@ -116,6 +116,9 @@ def main() -> int:
     ap.add_argument("--tiles-per-wave", type=float, default=1.0,
                     help="64-key tiles each wave of the profiled decode kernel takes (for --summarize-counters)")
     ap.add_argument("--note", default="", help="description line recorded in a counter summary")
+    ap.add_argument("--kernel-match", default="decode_attn_",
+                    help="kernel-name substring that picks the profiled kernel in --summarize-counters and "
+                         "--summarize-pmc (default: the decode kernels; prefill_attn_kernel for --prefill runs)")
     ap.add_argument("--summarize-probe", metavar="PROBE_JSON",
                     help="no GPU work: format the JSON line of a --stream-probe run (ceiling per grid, issue "
                          "cost, decode-step time and phases) as text")
@@ -123,7 +126,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.summarize_pmc:
-        print(summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.calib_copy_mib, args.cmd))
+        print(summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.calib_copy_mib, args.cmd,
+                            args.kernel_match))
         return 0
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.cmd))
@@ -132,7 +136,8 @@ def main() -> int:
         print(summarize_probe(args.summarize_probe))
         return 0
     if args.summarize_counters:
-        print(summarize_counters(args.summarize_counters, args.tiles_per_wave, args.note, args.cmd))
+        print(summarize_counters(args.summarize_counters, args.tiles_per_wave, args.note, args.cmd,
+                                 args.kernel_match))
         return 0
 
     if args.gpus != 1:
@@ -285,18 +290,7 @@ def main() -> int:
             return 1
 
     if args.calib_copy_mib:
-        # an elementwise kernel that reads n bytes and writes n bytes (bitwise
-        # not of uint8; a same-dtype copy_ would go to a DMA engine, which kernel
-        # counters do not see): the reference point that scales rocprof's
-        # FETCH_SIZE / WRITE_SIZE readings to bytes
-        n = args.calib_copy_mib << 20
-        src_buf = torch.zeros(n, dtype=torch.uint8, device=dev)
-        dst_buf = torch.empty_like(src_buf)
-        with torch.cuda.stream(stream):
-            for _ in range(3):
-                torch.bitwise_not(src_buf, out=dst_buf)
-        torch.cuda.synchronize()
-        del src_buf, dst_buf
+        calibration_copy(args.calib_copy_mib, dev, stream)
 
     kv_tokens = int((seq_lens + 1).sum().item()) if seq_lens is not None else B * attended
     a_bytes = attn_bytes(w, kv_tokens)
@@ -676,6 +670,23 @@ def stream_probe_bench(args, w: dict) -> int:
 MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 / fp16 matrix peak
 
 
+def calibration_copy(mib: int, dev, stream) -> None:
+    """An elementwise kernel that reads and writes mib MiB, three times (bitwise
+    not of uint8; a same-dtype copy_ would go to a DMA engine, which kernel
+    counters do not see): the reference point that scales rocprof's FETCH_SIZE
+    / WRITE_SIZE readings to bytes."""
+    import torch
+
+    n = mib << 20
+    src_buf = torch.zeros(n, dtype=torch.uint8, device=dev)
+    dst_buf = torch.empty_like(src_buf)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            torch.bitwise_not(src_buf, out=dst_buf)
+    torch.cuda.synchronize()
+    del src_buf, dst_buf
+
+
 def prefill_bench(args, w: dict) -> int:
     """Attention of a causal block of Sq query tokens over the workload's
     context (Sk keys, the block's own tokens last) on kvq_prefill_attn, with
@@ -726,6 +737,8 @@ def prefill_bench(args, w: dict) -> int:
     ms = timed(step, steps)
     ms_dense = timed(dense_step, max(1, steps // 2))
     err = (layers[0][5].float() - ops.dense_attention_over_quantized(*layers[0][:5], **kw).float()).abs().max().item()
+    if args.calib_copy_mib:
+        calibration_copy(args.calib_copy_mib, dev, torch.cuda.current_stream(dev))
     pairs = sum(min(Sk, Sk - Sq + i + 1) for i in range(Sq))  # admissible (query, key) pairs per head
     flops = 4.0 * B * Hq * D * pairs
     tfs = flops / (ms * 1e-3) / 1e12
@@ -860,14 +873,14 @@ def _pick(med: dict, counter: str, want) -> tuple:
     return best
 
 
-def summarize_pmc(fetch_csv: str, write_csv: str, calib_mib: int, cmd: str) -> str:
-    """Traffic summary: the attention kernel's FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch, median over dispatches), each scaled by expected / measured of the
-    same counter on the calibration kernel (bitwise not over calib_mib MiB, which
-    reads and writes calib_mib MiB)."""
+def summarize_pmc(fetch_csv: str, write_csv: str, calib_mib: int, cmd: str, match: str = "decode_attn_") -> str:
+    """Traffic summary: the attention kernel's (name containing `match`)
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch, median over dispatches), each
+    scaled by expected / measured of the same counter on the calibration kernel
+    (bitwise not over calib_mib MiB, which reads and writes calib_mib MiB)."""
     if calib_mib <= 0:
         raise SystemExit("--summarize-pmc needs --calib-copy-mib (the size the profiled run copied)")
-    is_attn = lambda n: "decode_attn_" in n and "merge" not in n
+    is_attn = lambda n: match in n and "merge" not in n
     is_copy = lambda n: "bitwise_not" in n
     out = []
     res = {}
@@ -888,11 +901,12 @@ def summarize_pmc(fetch_csv: str, write_csv: str, calib_mib: int, cmd: str) -> s
     return "\n".join([f"command: {cmd}" if cmd else "command: (not recorded)"] + out)
 
 
-def summarize_counters(path: str, tiles_per_wave: float, note: str, cmd: str) -> str:
-    """Counter summary of the decode kernel (the decode_attn_ kernel with the
-    most dispatches): for each counter its median per dispatch, that divided by
-    the dispatch's waves (Grid_Size / 64), and by tiles_per_wave; plus VALU
-    issue = SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES when both were collected."""
+def summarize_counters(path: str, tiles_per_wave: float, note: str, cmd: str, match: str = "decode_attn_") -> str:
+    """Counter summary of the profiled kernel (of the kernels whose name
+    contains `match`, the one with the most dispatches): for each counter its
+    median per dispatch, that divided by the dispatch's waves (Grid_Size / 64),
+    and by tiles_per_wave; plus VALU issue = SQ_ACTIVE_INST_VALU /
+    SQ_WAVE_CYCLES when both were collected."""
     import csv
     import statistics
 
@@ -901,12 +915,12 @@ def summarize_counters(path: str, tiles_per_wave: float, note: str, cmd: str) ->
     with open(path) as f:
         for row in csv.DictReader(f):
             name = row["Kernel_Name"]
-            if "decode_attn_" not in name:
+            if match not in name:
                 continue
             vals.setdefault(name, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
             grids.setdefault(name, []).append(int(row["Grid_Size"]))
     if not vals:
-        raise SystemExit("no decode_attn_ kernel in the counter input")
+        raise SystemExit(f"no kernel matching {match!r} in the counter input")
     name = max(vals, key=lambda n: len(grids[n]))
     waves = statistics.median(grids[name]) / 64.0
     out = [f"command: {cmd}" if cmd else "command: (not recorded)", f"kernel: {name[:110]}"]
