@@ -114,6 +114,38 @@ __device__ __forceinline__ float scale_f32(uint32_t bits) {
   return S_F16 ? f16_bits_to_f32(bits & 0xffffu) : bf16_bits_to_f32(bits & 0xffffu);
 }
 
+// The tile's share of one thread dequantized as (n - 8) sc directly (the
+// rare tiles with a scale beyond 2^125, where -8 sc would overflow): K code
+// dwords k (D / 32 of them used), V code words v (one per key), raw scales.
+template <int D, bool F16, bool S_F16, int KP, int VP>
+__device__ __attribute__((noinline)) void store_tile_direct(uint16_t* k_dst, uint16_t* v_dst, uint4 k,
+                                                            uint32_t ksc, uint4 v, uint4 vsc) {
+  constexpr int KB = D / 8, VD = D / 16;
+  const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
+  const float ksf = scale_f32<S_F16>(ksc);
+#pragma unroll
+  for (int w = 0; w < KB / 4; ++w) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t byte = (kw[w] >> (8 * j)) & 0xffu;
+      pk[j] = pack2<F16>((float)((int)(byte & 15u) - 8) * ksf, (float)((int)(byte >> 4) - 8) * ksf);
+    }
+    *(uint4*)(k_dst + 8 * w) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+  const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, vs[4] = {vsc.x, vsc.y, vsc.z, vsc.w};
+  float vf[4][VD];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float sc = scale_f32<S_F16>(vs[i]);
+#pragma unroll
+    for (int d = 0; d < VD; ++d) vf[i][d] = (float)((int)((vw[i] >> (4 * d)) & 15u) - 8) * sc;
+  }
+#pragma unroll
+  for (int d = 0; d < VD; ++d)
+    *(uint2*)(v_dst + d * VP) = make_uint2(pack2<F16>(vf[0][d], vf[1][d]), pack2<F16>(vf[2][d], vf[3][d]));
+}
+
 // RB = 16-row blocks per wave (1 or 2): with two, every K and V fragment read
 // from LDS feeds two MFMAs, halving LDS traffic and dequantize work per row.
 // Two row blocks per wave must stay within 256 registers (two waves per
@@ -156,6 +188,18 @@ void prefill_attn_kernel(const PrefillArgs a) {
     int l = row_ok[r] ? (a.causal ? a.Sk - a.Sq + s[r] + 1 : a.Sk) : 0;
     lim[r] = l < 0 ? 0 : (l > a.Sk ? a.Sk : l);
   }
+  // keys every row of the wave may attend: [0, lim_wave) (lim grows with the
+  // row, so this is the first row's; a wave with no row in the sequence
+  // masks nothing, its rows are never stored). Tiles inside it take the
+  // softmax without key masks.
+  int lim_wave;
+  {
+    const int R0 = blk * ROWS + __builtin_amdgcn_readfirstlane(wave) * 16 * RB;
+    const int s0 = R0 / a.ratio;
+    int l = a.causal ? a.Sk - a.Sq + s0 + 1 : a.Sk;
+    l = l < 0 ? 0 : (l > a.Sk ? a.Sk : l);
+    lim_wave = s0 < a.Sq ? l : 0x7fffffff;
+  }
   // keys any row of the workgroup attends
   const int r_last = min((blk + 1) * ROWS, a.Sq * a.ratio) - 1;
   int kend = a.causal ? a.Sk - a.Sq + r_last / a.ratio + 1 : a.Sk;
@@ -167,7 +211,14 @@ void prefill_attn_kernel(const PrefillArgs a) {
   const int tile_hi = min(tiles_all, tile_lo + tps);
 
   // the wave's queries as the B operand of S^T: lane (lq, lg) holds dims
-  // 32 kk + 8 lg .. + 7 of row lq (rows past Sq are zero)
+  // 32 kk + 8 lg .. + 7 of row lq (rows past Sq are zero). Scores reach the
+  // softmax as fma(s, c, -m) with c = |sm_scale| log2(e) > 0, so that the
+  // row max can be taken over the unscaled scores; a negative sm_scale
+  // negates the queries instead (a sign flip, exact).
+  // (c is kept above 0 so that the -inf scores of masked keys give 0, never
+  // NaN; sm_scale = 0 then weighs every key 2^(~1e-30 s) = 1, as it should)
+  const float c = fmaxf(fabsf(a.scale_log2), 1.0e-30f);
+  const uint32_t qneg = a.scale_log2 < 0.0f ? 0x80008000u : 0u;
   uint4 qf[RB][NK];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
@@ -178,7 +229,8 @@ void prefill_attn_kernel(const PrefillArgs a) {
       const uint16_t* p = qr + 32 * kk + 8 * lg;
       uint32_t x[4];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) x[w] = row_ok[r] ? (uint32_t)p[2 * w] | ((uint32_t)p[2 * w + 1] << 16) : 0u;
+      for (int w = 0; w < 4; ++w)
+        x[w] = row_ok[r] ? ((uint32_t)p[2 * w] | ((uint32_t)p[2 * w + 1] << 16)) ^ qneg : 0u;
       qf[r][kk] = make_uint4(x[0], x[1], x[2], x[3]);
     }
   }
@@ -250,35 +302,59 @@ void prefill_attn_kernel(const PrefillArgs a) {
       vsc[i] = __builtin_amdgcn_raw_buffer_load_b16(tvs, vr * vss2 + 2u * v_grp, 0, 0);
     }
   };
+  // Dequantize: (n - 8) sc rounded once to fp32, then to the operand type.
+  // With -8 sc exact (|sc| <= 2^125) that product is fma(n, sc, -8 sc), n
+  // taken straight from a byte of nibbles (v_cvt_f32_ubyte): two
+  // instructions an element. A wave holding a scale beyond 2^125 (or not
+  // finite) writes the tile again with the direct product, in a function of
+  // its own (inlined, a second copy of the tile code in the loop doubles the
+  // registers the compiler holds across it).
   auto store_tile = [&](int buf) {
+    uint16_t* k_dst = k_lds[buf] + k_key * KP + k_q * (D / 4);
+    uint16_t* v_dst = v_lds[buf] + (v_dq * VD) * VP + 4 * v_kq;
+    const float ksf = scale_f32<S_F16>(ksc);
+    bool wide = !(fabsf(ksf) <= 0x1p125f);
+    // the nibble mask through an empty asm: with the constant visible the
+    // compiler folds mask and byte select into a 4-bit extract, and then
+    // converts byte 0 of that (two instructions, not one v_cvt_f32_ubyteN)
+    uint32_t m4 = 0x0f0f0f0fu;
+    asm volatile("" : "+s"(m4));
     {  // K row k_key, dims k_q * D / 4 .. + D / 4 (element 2j of a byte's pair in the low nibble)
-      const float sc = scale_f32<S_F16>(ksc);
+      const float s8 = -8.0f * ksf;
       uint32_t pk[KB];
 #pragma unroll
-      for (int w = 0; w < KB / 4; ++w)
+      for (int w = 0; w < KB / 4; ++w) {
+        const uint32_t lo = kraw[w] & m4, hi = (kraw[w] >> 4) & m4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t byte = (kraw[w] >> (8 * j)) & 0xffu;
-          pk[4 * w + j] = pack2<F16>((float)((int)(byte & 15u) - 8) * sc, (float)((int)(byte >> 4) - 8) * sc);
-        }
-      uint16_t* dst = k_lds[buf] + k_key * KP + k_q * (D / 4);
+        for (int j = 0; j < 4; ++j)
+          pk[4 * w + j] = pack2<F16>(__builtin_fmaf((float)((lo >> (8 * j)) & 0xffu), ksf, s8),
+                                     __builtin_fmaf((float)((hi >> (8 * j)) & 0xffu), ksf, s8));
+      }
 #pragma unroll
       for (int w = 0; w < KB / 4; ++w)
-        *(uint4*)(dst + 8 * w) = make_uint4(pk[4 * w], pk[4 * w + 1], pk[4 * w + 2], pk[4 * w + 3]);
+        *(uint4*)(k_dst + 8 * w) = make_uint4(pk[4 * w], pk[4 * w + 1], pk[4 * w + 2], pk[4 * w + 3]);
     }
     {  // V^T rows v_dq * VD + d, keys 4 v_kq .. + 3
       float vf[4][VD];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float sc = scale_f32<S_F16>(vsc[i]);
+        wide = wide || !(fabsf(sc) <= 0x1p125f);
+        const float s8 = -8.0f * sc;
+        const uint32_t lo = vraw[i] & m4, hi = (vraw[i] >> 4) & m4;
 #pragma unroll
-        for (int d = 0; d < VD; ++d) vf[i][d] = (float)((int)((vraw[i] >> (4 * d)) & 15u) - 8) * sc;
+        for (int d = 0; d < VD; ++d)
+          vf[i][d] = __builtin_fmaf((float)((((d & 1) ? hi : lo) >> (8 * (d >> 1))) & 0xffu), sc, s8);
       }
 #pragma unroll
       for (int d = 0; d < VD; ++d)
-        *(uint2*)(v_lds[buf] + (v_dq * VD + d) * VP + 4 * v_kq) =
-            make_uint2(pack2<F16>(vf[0][d], vf[1][d]), pack2<F16>(vf[2][d], vf[3][d]));
+        *(uint2*)(v_dst + d * VP) = make_uint2(pack2<F16>(vf[0][d], vf[1][d]), pack2<F16>(vf[2][d], vf[3][d]));
     }
+    if (__builtin_amdgcn_ballot_w64(wide) != 0)
+      store_tile_direct<D, F16, S_F16, KP, VP>(k_dst, v_dst, make_uint4(kraw[0], kraw[1], kraw[KB / 4 > 2 ? 2 : 0],
+                                                                        kraw[KB / 4 > 2 ? 3 : 1]),
+                                               ksc, make_uint4(vraw[0], vraw[1], vraw[2], vraw[3]),
+                                               make_uint4(vsc[0], vsc[1], vsc[2], vsc[3]));
   };
 
   f32x4_t o[RB][NB];
@@ -330,25 +406,33 @@ void prefill_attn_kernel(const PrefillArgs a) {
       if (tile + 2 < tile_hi) load_tile((uint32_t)(t0 + 2 * kKeys));
     }
     // ---- online softmax (base 2) per query row; register j of block kb is
-    //      key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j ----
+    //      key t = t0 + 32 (kb / 2) + 8 lg + 4 (kb % 2) + j. Only tiles where
+    //      some row of the wave may not attend every key (the causal
+    //      diagonal, the sequence's last partial tile) set the scores of the
+    //      keys outside a row's range to -inf (weight exactly 0); the rest
+    //      skip the per-key compares and selects. ----
+    if (t0 + kKeys > lim_wave) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (t0 + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1) + j >= lim[r]) st[r][kb][j] = -__builtin_inff();
+    }
     uint2 pf[RB][4];
     float mt[RB];
     bool grow = false;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      const bool full = t0 + kKeys <= lim[r];  // no key of this tile is masked for this row
-      mt[r] = kNegP;
+      float mx = st[r][0][0];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float x = st[r][kb][j] * a.scale_log2;
-          if (!full) x = t0 + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1) + j < lim[r] ? x : kNegP;
-          st[r][kb][j] = x;
-          mt[r] = fmaxf(mt[r], x);
-        }
-      mt[r] = fmaxf(mt[r], __shfl_xor(mt[r], 16));
-      mt[r] = fmaxf(mt[r], __shfl_xor(mt[r], 32));
+        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, st[r][kb][j]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mt[r] = mx * c;  // -inf if no key of the tile is in the row's range
       grow = grow || mt[r] > m_run[r] + kLazyMaxP;
     }
     // lazy running max: the state is rescaled only in tiles where some row
@@ -366,14 +450,12 @@ void prefill_attn_kernel(const PrefillArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      const bool full = t0 + kKeys <= lim[r];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         float p[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(st[r][kb][j] - m_run[r]);
-          if (!full) p[j] = st[r][kb][j] > kNegP ? p[j] : 0.0f;
+          p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r][kb][j], c, -m_run[r]));
           l_run[r] += p[j];
         }
         pf[r][kb] = make_uint2(pack2<F16>(p[0], p[1]), pack2<F16>(p[2], p[3]));

@@ -22,9 +22,13 @@ argmax, every decode step < 2.0, and the same greedy token at >= 48 of the
 64 steps (56 measured; the reference's generate test asks a prefix of 4 of
 16, tests/llama3/test_llama3_generate_parity.py:52-74). The prefill argmax is
 compared exactly when F's top-2 logit margin exceeds twice the measured
-max-abs difference. Below that, a different attention kernel can swap a
-near-tie, and Q's token must then be F's runner-up. On this prompt F's margin
-is 0.031, against 0.33 between Q's matrix-core prefill and F's flash SDPA.
+max-abs difference d0. Below that, a different attention kernel can reorder
+a near-tie, and Q's token must then be one F scores within 2 d0 of its best.
+On this prompt F's margin is 0.031, against d0 = 0.32 between Q's
+matrix-core prefill and F's flash SDPA. As distributions, Q stays close to
+F: KL(F || Q) <= 0.02 nats at the prefill and every step (measured 0.0034
+at most), and their top-10 tokens share 8 on average, 6 at least (measured
+8.9 and 6).
 
 Q against R (INT4 against the bf16 DynamicCache, the north star's check) has
 its own stated tolerance: this random-init network amplifies the INT4
@@ -34,9 +38,13 @@ so the reference's absolute bars (set on pretrained models) cannot hold
 against R for any INT4 implementation here, including the reference's own
 semantics F. The bound is therefore relative to what the format itself
 costs, measured in the same run: at the prefill and at every decode step,
-max-abs(Q - R) <= max-abs(F - R) + 0.5, and Q's greedy tokens agree with R's
-at no fewer steps than F's do, minus 4 of 64. (Rounding K/V to fp16 instead
-of INT4 moves the logits by 0.07, so the gap is the 4-bit format's.)
+max-abs(Q - R) <= max-abs(F - R) + 0.5, and, on the next-token
+distributions, KL(R || Q) <= 1.05 KL(R || F) + 0.01 nats (measured: KL(R ||
+F) 0.53 on average, Q's worst step 0.8 % and 0.005 nats above F's). Greedy
+agreement with R says nothing here (F itself agrees at 1 of 64 steps: the
+random network's greedy path leaves R's after the first token), nor does
+top-10 overlap with R (0.75 of 10 for F). (Rounding K/V to fp16 instead of
+INT4 moves the logits by 0.07, so the gap is the 4-bit format's.)
 The test also prints ms per decode token of Q (HF eager, Python overhead
 included) and the KV bytes of both caches.
 """
@@ -98,6 +106,19 @@ def _diffs(a, b):
     return [(x - y).abs().max().item() for x, y in zip(a, b)]
 
 
+def _kl(p_logits, q_logits) -> float:
+    """KL(P || Q) of the next-token distributions softmax(logits), float64."""
+    lp = torch.log_softmax(p_logits.double(), -1)
+    lq = torch.log_softmax(q_logits.double(), -1)
+    return float((lp.exp() * (lp - lq)).sum(-1).max())
+
+
+def _top_overlap(a_logits, b_logits, k=10) -> int:
+    """Tokens common to the top-k of both."""
+    ta = set(a_logits[0].topk(k).indices.tolist())
+    return len(ta & set(b_logits[0].topk(k).indices.tolist()))
+
+
 def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
     torch.manual_seed(2)
     prev = torch.get_default_dtype()
@@ -140,6 +161,14 @@ def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
         d0_fr = (first_r - first_f).abs().max().item()
         diffs_fr = _diffs(logits_r, logits_f)
         agree_fr = int((own_r == own_f).sum().item())
+        # next-token distributions against R, at the prefill and every step
+        kl_q = [_kl(first_r, first_q)] + [_kl(r, q) for r, q in zip(logits_r, logits_q)]
+        kl_f = [_kl(first_r, first_f)] + [_kl(r, f) for r, f in zip(logits_r, logits_f)]
+        ov_q = [_top_overlap(first_r, first_q)] + [_top_overlap(r, q) for r, q in zip(logits_r, logits_q)]
+        ov_f = [_top_overlap(first_r, first_f)] + [_top_overlap(r, f) for r, f in zip(logits_r, logits_f)]
+        # and Q against F, the semantics it implements
+        kl_fq = [_kl(first_f, first_q)] + [_kl(f, q) for f, q in zip(logits_f, logits_q)]
+        ov_fq = [_top_overlap(first_f, first_q)] + [_top_overlap(f, q) for f, q in zip(logits_f, logits_q)]
         print(f"C3 INT4 (Q) vs INT4 dense reference (F): prefill last-logit max-abs {d0:.4f}; decode max-abs "
               f"max {max(diffs):.4f} mean {statistics.fmean(diffs):.4f}; same greedy token {agree}/{STEPS}")
         print(f"C3 INT4 (Q) vs bf16 DynamicCache (R): prefill max-abs {d0_r:.4f}; decode max-abs max "
@@ -148,6 +177,13 @@ def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
         print(f"C3 INT4 dense reference (F) vs bf16 DynamicCache (R): prefill max-abs {d0_fr:.4f}; decode "
               f"max-abs max {max(diffs_fr):.4f} mean {statistics.fmean(diffs_fr):.4f}; same greedy token "
               f"{agree_fr}/{STEPS}")
+        print(f"C3 KL(R || Q) mean {statistics.fmean(kl_q):.4f} max {max(kl_q):.4f}; KL(R || F) mean "
+              f"{statistics.fmean(kl_f):.4f} max {max(kl_f):.4f}; worst step ratio "
+              f"{max(q / f for q, f in zip(kl_q, kl_f)):.3f}, worst excess {max(q - f for q, f in zip(kl_q, kl_f)):.4f}")
+        print(f"C3 top-10 overlap with R: Q mean {statistics.fmean(ov_q):.2f} min {min(ov_q)}; F mean "
+              f"{statistics.fmean(ov_f):.2f} min {min(ov_f)}")
+        print(f"C3 Q vs F: KL(F || Q) mean {statistics.fmean(kl_fq):.5f} max {max(kl_fq):.5f}; top-10 overlap "
+              f"mean {statistics.fmean(ov_fq):.2f} min {min(ov_fq)}")
         print(f"C3 INT4 decode ms/token median {1e3 * statistics.median(secs_q):.2f} (HF eager); KV bytes: "
               f"DynamicCache {ref_kv_bytes / 2**20:.0f} MiB, INT4 {q_cache.nbytes() / 2**20:.0f} MiB")
         top2 = first_f[0].topk(2)
@@ -156,11 +192,11 @@ def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
               f"Q {first_q.argmax().item()}")
         assert d0 < 1.0
         # same first token, or (a near-tie in F, closer than the logit change
-        # between two attention kernels) F's runner-up
+        # between two attention kernels) a token F scores within 2 d0 of its best
         if gap > 2 * d0:
             assert first_f.argmax().item() == first_q.argmax().item()
         else:
-            assert first_q.argmax().item() in top2.indices.tolist()
+            assert first_f[0, first_q.argmax().item()].item() >= top2.values[0].item() - 2 * d0
         for step, d in enumerate(diffs):
             assert d < 2.0, f"decode step {step}: {d}"
         assert agree >= 48, f"Q and F pick the same greedy token at {agree} of {STEPS} steps"
@@ -168,7 +204,13 @@ def test_c3_llama31_8b_16k_prefill_and_64_decode_steps():
         assert d0_r <= d0_fr + 0.5, f"prefill: |Q - R| {d0_r:.3f} > |F - R| {d0_fr:.3f} + 0.5"
         for step, (dq, df) in enumerate(zip(diffs_r, diffs_fr)):
             assert dq <= df + 0.5, f"decode step {step}: |Q - R| {dq:.3f} > |F - R| {df:.3f} + 0.5"
-        assert agree_r >= agree_fr - 4, f"greedy agreement with R: Q {agree_r}, F {agree_fr}" 
+        # next-token distributions: Q is no further from R than the format
+        # itself puts F (KL within 5 % + 0.01 nats at every step; measured
+        # 0.8 % and 0.005), and close to F (KL <= 0.02 nats, top-10 sharing 7+)
+        for step, (kq, kf) in enumerate(zip(kl_q, kl_f)):
+            assert kq <= 1.05 * kf + 0.01, f"step {step - 1}: KL(R || Q) {kq:.4f} > 1.05 KL(R || F) {kf:.4f} + 0.01"
+        assert max(kl_fq) <= 0.02, f"KL(F || Q) {max(kl_fq):.4f}"
+        assert statistics.fmean(ov_fq) >= 8 and min(ov_fq) >= 6, ov_fq
     finally:
         del model
         torch.cuda.empty_cache()

@@ -146,3 +146,55 @@ def test_prefill_random_shapes(seed):
     assert np.isfinite(got).all()
     err = np.abs(got - _oracle(q, kp, ks, vp, vs, G, causal)).max()
     assert err <= 2e-2, err
+
+
+@pytest.mark.parametrize("sm_scale", [-(128 ** -0.5), 0.0, 0.02])
+def test_prefill_any_softmax_scale(sm_scale):
+    """The kernel takes the row max over unscaled scores and scales with
+    fma(s, |c|, -m); a negative sm_scale negates the queries instead, and 0
+    weighs every admissible key alike. Causal prompt chunk (diagonal tiles
+    masked, the rest not) against the fp64 oracle at the same scale."""
+    B, Hq, Hkv, Sq, Sk, D, G = 1, 8, 2, 150, 300, 128, 32
+    print(f"prefill sm_scale {sm_scale}", flush=True)
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, Sq, Sk, D, "bf16", G, seed=91)
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=True,
+                                sm_scale=sm_scale)
+    want = O.attention_over_quantized(
+        q.float().numpy(), kp.cpu().numpy(), ks.float().cpu().numpy(), vp.cpu().numpy(),
+        vs.float().cpu().numpy(), group_size=G, scale=sm_scale, is_causal=True)
+    err = np.abs(out.float().cpu().numpy() - want).max()
+    print(f"prefill sm_scale {sm_scale}: max-abs {err:.2e}")
+    assert err <= 2e-2, err
+    dense = ops.dense_attention_over_quantized(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G,
+                                               is_causal=True, sm_scale=sm_scale)
+    assert (out.float() - dense.float()).abs().max().item() <= 2e-2
+
+
+def test_prefill_scales_beyond_2_pow_125():
+    """Dequantization runs as fma(n, sc, -8 sc), exact while -8 sc does not
+    overflow; a tile holding a scale above 2^125 is written again as
+    (n - 8) sc. One key's values carry a bf16 scale of 4.5e37 (codes 1..15:
+    |(n - 8) sc| <= 3.2e38, finite) and a key row of -2 that keeps its weight
+    near 1e-7, so that its values dominate every output without overflowing.
+    The fma form would turn that key's values into -inf."""
+    B, Hq, Hkv, Sq, Sk, D, G = 1, 4, 1, 64, 128, 128, 32
+    g = torch.Generator().manual_seed(5)
+    q = torch.full((B, Hq, Sq, D), 0.5).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, Sk, D, generator=g)
+    k[:, :, 77] = -2.0
+    v = torch.randn(B, Hkv, Sk, D, generator=g)
+    kp, ks = ops.quantize(k.to(torch.bfloat16).to(DEV), G, torch.bfloat16)
+    vp, vs = ops.quantize(v.to(torch.bfloat16).to(DEV), G, torch.bfloat16)
+    codes = torch.randint(1, 16, (B, Hkv, D), generator=g, dtype=torch.int32)
+    vp[:, :, 77] = (codes[..., 0::2] | (codes[..., 1::2] << 4)).to(torch.uint8).to(DEV)
+    vs[:, :, 77] = torch.tensor(4.5e37, dtype=torch.bfloat16)
+    assert float(vs[0, 0, 77, 0]) > 2.0 ** 125
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=False,
+                                sm_scale=D ** -0.5)
+    got = out.float().cpu().numpy()
+    want = O.attention_over_quantized(
+        q.float().numpy(), kp.cpu().numpy(), ks.float().cpu().numpy(), vp.cpu().numpy(),
+        vs.float().cpu().numpy(), group_size=G, is_causal=False)
+    assert np.isfinite(want).all() and np.abs(want).max() > 1e25
+    assert np.isfinite(got).all()
+    assert np.all(np.abs(got - want) <= 2e-2 + 3e-2 * np.abs(want))
