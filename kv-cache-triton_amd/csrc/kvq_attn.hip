@@ -32,7 +32,9 @@
 //   * PV: lane (token subset ts, dim block j) holds codes of 4 tokens x 1 dim
 //     per instruction (B) and reads A = softmax weights w = p * v_scale of 4
 //     rows x the same 4 tokens from LDS. All 4 lanes of a block share one
-//     32-dim chunk, so the per-chunk value scale rides in A.
+//     32-dim chunk, so the per-chunk value scale rides in A: bf16 weights,
+//     or for fp16 models fp16 weights, with the power of two of the 4
+//     tokens' largest scale carried by the code operand (PV16 below).
 //   The VALU only converts nibbles to bf16/fp16 and runs the softmax.
 // decode_attn_valu_kernel (fp32 queries or fp32 scales) keeps exact fp32
 //   arithmetic (v_fmac) for the 1e-4 bar of fp32 inputs; MHA-sized row counts.
@@ -42,7 +44,9 @@
 //   bf16: scores accumulate q*(128+n) on top of an initial -136*sum(q) per
 //         chunk; values accumulate w*(128+n) and subtract 136*sum(w) at the
 //         end, sum(w) coming from one extra MFMA on the same rounded weights.
-//   fp16: (1024+n) - 1032 = n - 8 exactly (v_pk_add_f16), no correction.
+//   fp16: scores take the same form with 1024 + n and -1032; values (PV16)
+//         accumulate w*2^(E-25)(1024+n) and subtract the same product with
+//         n = 8, one extra MFMA.
 // Softmax runs in base 2 with sm_scale*log2(e) folded into the key scale.
 #include <algorithm>
 #include <cmath>
@@ -692,6 +696,25 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   constexpr uint32_t NEG_BIAS = F16 ? 0xE408E408u : 0xC308C308u;  // {-1032, -1032} / {-136, -136}
   constexpr uint32_t SEL_02 = 0x04010400u;  // {MAGIC | byte0, MAGIC | byte1}
   constexpr uint32_t SEL_46 = 0x04030402u;  // {MAGIC | byte2, MAGIC | byte3}
+  // PV in fp16 for fp16 models (fp16 queries and scales). A bf16 weight
+  // p * v_scale keeps 8 significant bits, below what an fp16 output holds;
+  // an fp16 weight keeps 11, but p * v_scale overflows fp16 for large scales.
+  // So the scales' power of two moves into the code operand instead, per
+  // group of four tokens that share a matrix block (token subset ts of a
+  // subtile): with E = clamp(e + 10, 11, 30), e the fp16 exponent field of
+  // the group's largest |v_scale| (over its tokens and chunks), the operand
+  // fp16 {E, code n} is 2^(E - 25) (1024 + n), and a weight is p * v_scale *
+  // 2^(25 - E): below 2p for the largest scale (a scale under 64), at most
+  // p * 2047 otherwise. The running-max slack drops to 5 (p <= 32) so that
+  // this stays within fp16's 65504. Weights of much smaller scales reach
+  // fp16's subnormal range only where they are negligible against the
+  // group's largest. The bias term is the same product with every code at 8
+  // (operand 2^(E - 25) 1032); o and the bias accumulate p * v_scale * (1024
+  // + n) and p * v_scale * 1032 whatever E a group took. The group's E << 2
+  // goes through LDS to the PV lanes of its subset, one byte per subtile.
+  constexpr bool PV16 = F16 && S_F16;
+  constexpr float LAZY = PV16 ? 5.0f : kLazyMax;
+  constexpr float PV_BIAS = PV16 ? -1.0f : -136.0f;
 
   // Per wave: the softmax weights of the tile, [rowset][subtile] blocks of
   // 4 * LPT * VTS * 4 bf16 in which (row, chunk) pair rc = 4 * chunk + row,
@@ -720,6 +743,8 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // values (two elements per lane of the V wave)
   __shared__ __attribute__((aligned(16))) float nt_lds[RS * 4 + 128];
   auto w_lds = reinterpret_cast<uint16_t(*)[RS][NSUB][4 * LPT * VTS * 4]>(smem);
+  static_assert(NSUB <= 4, "one exponent byte per subtile in a dword");
+  __shared__ __attribute__((aligned(4))) uint8_t hb_lds[PV16 ? NW : 1][VTS][4];
   auto o_lds = reinterpret_cast<float(*)[ROWS][D]>(smem);
 
   const int tid = threadIdx.x;
@@ -1255,6 +1280,32 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       }
       if (refill) load_k(i, base + NW * CH);
 
+      // PV16: the tile's V scales per chunk of this lane's token and its
+      // group's exponent (the scale rows arrive right after the keys)
+      float svl[LPT];
+      if constexpr (PV16) {
+        chunk_scales<LPT, S_F16>(svr[i], g32, gsh, 1.0f, svl);
+        float smax = fabsf(svl[0]);
+#pragma unroll
+        for (int c = 1; c < LPT; ++c) smax = fmaxf(smax, fabsf(svl[c]));
+        // over the group: the lanes VTS apart in the token's SUB-lane subtile
+        if constexpr (VTS == 4) {  // D = 128: lanes ts + 4k of a 16-lane row
+          smax = fmaxf(smax, dpp<0x124>(smax, 0.0f));  // row_ror:4
+          smax = fmaxf(smax, dpp<0x128>(smax, 0.0f));  // row_ror:8
+        } else {  // D = 64: lanes ts + 8k of two 16-lane rows
+          smax = fmaxf(smax, dpp<0x128>(smax, 0.0f));  // row_ror:8
+          float other = smax;
+          permlane16_swap(smax, other);
+          smax = fmaxf(smax, other);
+        }
+        // fp32 exponent field e32 = e + 112 for a normal fp16 scale
+        const int e32 = (int)((__builtin_bit_cast(uint32_t, smax) >> 23) & 0xffu);
+        const int E = min(max(e32 - 102, 11), 30);
+#pragma unroll
+        for (int c = 0; c < LPT; ++c) svl[c] = __builtin_amdgcn_ldexpf(svl[c], 25 - E);
+        hb_lds[wave][w_ts][w_sub] = (uint8_t)(E << 2);
+      }
+
       // ---- tile max, rescale of the running state (not for a wave's
       //      first tile: its accumulators are still zero). The running max
       //      is a reference, not the exact maximum: it moves (and the state
@@ -1276,7 +1327,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
 #pragma unroll
           for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) grow = grow || (mt[rs][r] > m_run[rs][r] + kLazyMax);
+            for (int r = 0; r < 4; ++r) grow = grow || (mt[rs][r] > m_run[rs][r] + LAZY);
           if (grow) {
 #pragma unroll
             for (int rs = 0; rs < RS; ++rs) {
@@ -1297,10 +1348,10 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
         fresh = false;
       }
 
-      // ---- p and w = p * v_scale (bf16) -> LDS ----
+      // ---- p and w = p * v_scale (bf16; PV16: fp16, the tile's largest
+      //      scale's power of two moved into the code operand) -> LDS ----
       {
-        float svl[LPT];
-        chunk_scales<LPT, S_F16>(svr[i], g32, gsh, 1.0f, svl);
+        if constexpr (!PV16) chunk_scales<LPT, S_F16>(svr[i], g32, gsh, 1.0f, svl);
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
@@ -1311,8 +1362,14 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
             l_acc[rs][r] += p;
 #pragma unroll
             for (int c = 0; c < LPT; c += 2) {
-              const bf16x2_t pk2 = {(__bf16)(p * svl[c]), (__bf16)(p * svl[c + 1])};
-              const uint32_t pk = __builtin_bit_cast(uint32_t, pk2);
+              uint32_t pk;
+              if constexpr (PV16) {
+                const f16x2_t pk2 = {(_Float16)(p * svl[c]), (_Float16)(p * svl[c + 1])};
+                pk = __builtin_bit_cast(uint32_t, pk2);
+              } else {
+                const bf16x2_t pk2 = {(__bf16)(p * svl[c]), (__bf16)(p * svl[c + 1])};
+                pk = __builtin_bit_cast(uint32_t, pk2);
+              }
               w_lds[wave][rs][w_sub][(((4 * c + r) ^ w_sub) * VTS + w_ts) * 4 + w_k] = (uint16_t)pk;
               w_lds[wave][rs][w_sub][(((4 * c + 4 + r) ^ w_sub) * VTS + w_ts) * 4 + w_k] = (uint16_t)(pk >> 16);
             }
@@ -1327,8 +1384,15 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       if (i == 0 && base == wave) KVQ_STAMP_AFTER(3, vq[i][NSUB - 1][3]);
       // u = bytes {t0.b, t1.b, t0.b', t1.b'} of two tokens' code dwords; its low
       // and high nibbles then give (token0, token1) pairs of one dim per perm.
+      // PV16: the exponent bytes of this lane's subset, one per subtile
+      const uint32_t hbd = PV16 ? *(const uint32_t*)&hb_lds[wave][vts][0] : 0u;
 #pragma unroll
       for (int s = 0; s < NSUB; ++s) {
+        // the operands' high bytes: bf16 128 + n, or (PV16) {E | n} with
+        // byte s of hbd
+        const uint32_t hb = PV16 ? hbd : 0x43434343u;
+        const uint32_t s02 = PV16 ? ((0x04u + s) << 24) | (0x01u << 16) | ((0x04u + s) << 8) : SEL_02;
+        const uint32_t s46 = PV16 ? ((0x04u + s) << 24) | (0x03u << 16) | ((0x04u + s) << 8) | 0x02u : SEL_46;
         uint32_t bp[2][8];  // [token pair][dim within the lane's 8]
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
@@ -1337,10 +1401,10 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
           for (int hh = 0; hh < 2; ++hh) {  // dims 0-3, dims 4-7
             const uint32_t u = __builtin_amdgcn_perm(v1, v0, hh ? 0x07030602u : 0x05010400u);
             const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
-            bp[tp][4 * hh + 0] = __builtin_amdgcn_perm(0x43434343u, lo, SEL_02);
-            bp[tp][4 * hh + 1] = __builtin_amdgcn_perm(0x43434343u, hi, SEL_02);
-            bp[tp][4 * hh + 2] = __builtin_amdgcn_perm(0x43434343u, lo, SEL_46);
-            bp[tp][4 * hh + 3] = __builtin_amdgcn_perm(0x43434343u, hi, SEL_46);
+            bp[tp][4 * hh + 0] = __builtin_amdgcn_perm(hb, lo, s02);
+            bp[tp][4 * hh + 1] = __builtin_amdgcn_perm(hb, hi, s02);
+            bp[tp][4 * hh + 2] = __builtin_amdgcn_perm(hb, lo, s46);
+            bp[tp][4 * hh + 3] = __builtin_amdgcn_perm(hb, hi, s46);
           }
         }
 #pragma unroll
@@ -1348,8 +1412,11 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
           const uint2 wa = *(const uint2*)&w_lds[wave][rs][s][((v_rc ^ s) * VTS + vts) * 4];
 #pragma unroll
           for (int m = 0; m < 8; ++m)
-            o_acc[rs][m] = mfma4<false>(wa.x, wa.y, bp[0][m], bp[1][m], o_acc[rs][m]);
-          w_acc[rs] = mfma4<false>(wa.x, wa.y, kBf16OnePair, kBf16OnePair, w_acc[rs]);
+            o_acc[rs][m] = mfma4<PV16>(wa.x, wa.y, bp[0][m], bp[1][m], o_acc[rs][m]);
+          // the bias sum: weights times 1 (bf16, taken 136 times later), or
+          // (PV16) times the code operand of n = 8
+          const uint32_t bias_pair = PV16 ? __builtin_amdgcn_perm(hb, 0x08080808u, s02) : kBf16OnePair;
+          w_acc[rs] = mfma4<PV16>(wa.x, wa.y, bias_pair, bias_pair, w_acc[rs]);
         }
       }
       if (refill) load_v(i, base + NW * CH);
@@ -1376,7 +1443,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
       for (int m = 0; m < 8; ++m)
-        val[(rs * 4 + r) * 8 + m] = fmaf(-136.0f, w_acc[rs][r], o_acc[rs][m][r]);
+        val[(rs * 4 + r) * 8 + m] = fmaf(PV_BIAS, w_acc[rs][r], o_acc[rs][m][r]);
 #pragma unroll
   for (int i = 0; i < NV / 2; ++i) {
     float x = val[i], y = val[i + NV / 2];
