@@ -1274,7 +1274,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
             for (int r = 0; r < 4; ++r) {
               bool ok = t < t_end;
               if constexpr (ROWMASK) ok = ok && (t < lim[rs][r]);
-              sc[rs][r] = ok ? sc[rs][r] : kNeg;
+              sc[rs][r] = ok ? sc[rs][r] : (ROWMASK ? kNeg : -__builtin_inff());
             }
         }
       }
@@ -1357,8 +1357,13 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float s = sc[rs][r];
+            // Masked keys: without row masks they score -inf, and a wave's
+            // first tile holds a key of the split, so every row's running max
+            // is finite and the weight 2^(-inf - m) is 0 with no select. With
+            // row masks a row may have no key yet (max kNeg): they score kNeg
+            // and their weight is set to 0.
             float p = __builtin_amdgcn_exp2f(s - m_run[rs][r]);
-            if (masked) p = s > kNeg ? p : 0.0f;
+            if constexpr (ROWMASK) p = s > kNeg ? p : 0.0f;
             l_acc[rs][r] += p;
 #pragma unroll
             for (int c = 0; c < LPT; c += 2) {
