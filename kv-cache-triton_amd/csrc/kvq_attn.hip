@@ -1173,7 +1173,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       am = fmax_nc(u, v);
     }
     const float scale = group_scale(am);  // am / 7, correctly rounded
-    const float inv = 1.0f / scale;
+    const float inv = group_inverse(scale);
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
     float c0 = rint_quotient(x0, scale, inv, fast), c1 = rint_quotient(x1, scale, inv, fast);
     c0 = fminf(fmaxf(c0, -8.0f), 7.0f);
@@ -1693,7 +1693,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
       am = fmax_nc(u, v);
     }
     const float scale = group_scale(am);  // am / 7, correctly rounded
-    const float inv = 1.0f / scale;
+    const float inv = group_inverse(scale);
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
     float c0 = rint_quotient(x0, scale, inv, fast), c1 = rint_quotient(x1, scale, inv, fast);
     c0 = fminf(fmaxf(c0, -8.0f), 7.0f);

@@ -46,17 +46,21 @@ __device__ __forceinline__ float group_scale(float am) {
 }
 
 // rint(x / s) where x / s is the IEEE (correctly rounded) fp32 quotient, for
-// |x| <= 7 s (x an element of the group whose absmax / 7 is s, s normal):
-// t = x * (1 / s), both steps correctly rounded, lies within 2^-19.6 of the
-// rounded quotient (relative error 2^-23 on |x / s| <= 7, plus the quotient's
-// own rounding of 2^-21), so rint(t) is rint of the quotient unless t is
-// within that distance of a half-integer; those rare elements (and groups
-// whose scale is not a moderate normal number) take the division itself. The
-// threshold used, 2^-17, leaves a margin of 6x.
+// |x| <= 7 s (x an element of the group whose absmax / 7 is s, s a moderate
+// normal number): with inv = v_rcp_f32(s), within 1 ulp of 1 / s (relative
+// 2^-23; the instruction's documented accuracy), t = RN(x * inv) differs from
+// x / s by a relative 2^-23 + 2^-24 and from the rounded quotient by at most
+// 7 (2^-23 + 2^-24 + 2^-24) = 7 * 2^-22 ~ 2^-19.2 on |x / s| <= 7, so rint(t)
+// is rint of the quotient unless t lies within that distance of a
+// half-integer. Such elements (and groups whose scale is not in [2^-100,
+// 2^100]) take the division itself. The threshold used, 2^-17, leaves a
+// margin of 4.6x (3x for an inverse off by 2 ulp).
+__device__ __forceinline__ float group_inverse(float s) { return __builtin_amdgcn_rcpf(s); }
+__device__ __forceinline__ bool near_half(float t, float r) { return fabsf(t - r) > 0.5f - 0x1p-17f; }
 __device__ __forceinline__ float rint_quotient(float x, float s, float inv, bool fast) {
   const float t = x * inv;
   const float r = __builtin_rintf(t);
-  if (fast && !(fabsf(t - r) > 0.5f - 0x1p-17f)) return r;
+  if (fast && !near_half(t, r)) return r;
   return __builtin_rintf(x / s);
 }
 

@@ -35,6 +35,9 @@ struct QuantArgs {
   int64_t cap;  // contiguous layout: destination rows per (b, h); rows at or past it are dropped
   int x_dtype, scale_dtype;
   PageMap pm;  // pm.paged: packed/scales are pools (ps_b = ss_b = 0)
+  // row -> (b, h, s) and thread -> (row, chunk) without runtime divides
+  // (vector path; rows * D / 8 < 2^32)
+  FastDiv div_s, div_h, div_cpr;
 };
 
 // Destination row of (b, position), or -1 where it does not exist: the
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
   const uint32_t rows = (uint32_t)a.rows;
   const uint32_t rq = (rows + RPT - 1) / RPT;
   const bool slot = idx < rq * cpr;
-  const uint32_t r0 = slot ? idx / cpr : 0u;
+  const uint32_t r0 = slot ? fdiv(idx, a.div_cpr) : 0u;
   const uint32_t ch = slot ? idx - r0 * cpr : 0u;
   const uint32_t S = (uint32_t)a.S, H = (uint32_t)a.H;
 
@@ -148,10 +151,10 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     const uint32_t row = r0 + (uint32_t)k * rq;
     live[k] = slot && row < rows;
     const uint32_t rw = live[k] ? row : 0u;
-    ss[k] = rw % S;
-    const uint32_t bh = rw / S;
-    hh[k] = bh % H;
-    bb[k] = bh / H;
+    const uint32_t bh = fdiv(rw, a.div_s);
+    ss[k] = rw - bh * S;
+    bb[k] = fdiv(bh, a.div_h);
+    hh[k] = bh - bb[k] * H;
     const int64_t xoff = (int64_t)bb[k] * a.xs_b + (int64_t)hh[k] * a.xs_h + (int64_t)ss[k] * a.xs_s + 8 * ch;
 #pragma unroll
     for (int n = 0; n < NW; ++n)
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     if constexpr (LPG >= 16) amax = fmaxf(amax, dpp_f<0x140>(amax)); // row_mirror
     if (!live[k]) continue;
     const float scale = group_scale(amax);  // amax / 7, correctly rounded
-    const float inv = 1.0f / scale;
+    const float inv = group_inverse(scale);
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
     uint32_t word = 0;
 #pragma unroll
@@ -238,6 +241,7 @@ struct DequantArgs {
   int64_t os_b, os_h, os_s, os_d;
   int scale_dtype, out_dtype;
   PageMap pm;  // pm.paged: packed/scales are pools (ps_b = ss_b = 0)
+  FastDiv div_s, div_h, div_cpr;  // as in QuantArgs (vector path)
 };
 
 __global__ __launch_bounds__(256) void dequantize_kernel(const DequantArgs a) {
@@ -281,7 +285,7 @@ __global__ __launch_bounds__(256) void dequantize_vec_kernel(const DequantArgs a
   const uint32_t rows = (uint32_t)a.rows;
   const uint32_t rq = (rows + RPT - 1) / RPT;
   if (idx >= rq * cpr) return;
-  const uint32_t r0 = idx / cpr;
+  const uint32_t r0 = fdiv(idx, a.div_cpr);
   const uint32_t ch = idx - r0 * cpr;
   const uint32_t S = (uint32_t)a.S, H = (uint32_t)a.H;
   uint32_t w[RPT];
@@ -294,9 +298,9 @@ __global__ __launch_bounds__(256) void dequantize_vec_kernel(const DequantArgs a
     const uint32_t row = r0 + (uint32_t)k * rq;
     live[k] = row < rows;
     const uint32_t rw = live[k] ? row : 0u;
-    const uint32_t s = rw % S, bh = rw / S;
-    hh[k] = bh % H;
-    bb[k] = bh / H;
+    const uint32_t bh = fdiv(rw, a.div_s), s = rw - bh * S;
+    bb[k] = fdiv(bh, a.div_h);
+    hh[k] = bh - bb[k] * H;
     pos[k] = s;
     obase[k] = (int64_t)bb[k] * a.os_b + (int64_t)hh[k] * a.os_h + (int64_t)s * a.os_s + 8 * ch;
   }
@@ -433,6 +437,9 @@ int quantize_impl(const char* who, const void* x, int x_dtype, const int64_t* x_
   a.cap = capacity;
   a.x_dtype = x_dtype; a.scale_dtype = scale_dtype;
   a.pm = pm;
+  a.div_s = make_fastdiv((uint32_t)S);
+  a.div_h = make_fastdiv((uint32_t)H);
+  a.div_cpr = make_fastdiv((uint32_t)std::max<int64_t>(1, D / 8));
 
   hipStream_t st = (hipStream_t)stream;
   const int lpg = (int)(group_size / 8);
@@ -496,6 +503,9 @@ int dequantize_impl(const void* packed, const int64_t* packed_strides,
   a.os_b = out_strides[0]; a.os_h = out_strides[1]; a.os_s = out_strides[2]; a.os_d = out_strides[3];
   a.scale_dtype = scale_dtype; a.out_dtype = out_dtype;
   a.pm = pm;
+  a.div_s = make_fastdiv((uint32_t)S);
+  a.div_h = make_fastdiv((uint32_t)H);
+  a.div_cpr = make_fastdiv((uint32_t)std::max<int64_t>(1, d_out / 8));
 
   const int64_t oes = dtype_size(out_dtype);
   const bool vec = group_size % 8 == 0 && d_out == num_groups * group_size && a.os_d == 1 &&
