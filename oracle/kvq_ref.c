@@ -243,3 +243,61 @@ int64_t kvqref_check_div7(uint32_t lo, uint32_t hi) {
   }
   return bad;
 }
+
+/* Pins the divide-free rounding of the quantize kernels (rint_quotient in
+ * kv-cache-triton_amd/csrc/kvq_common.h): with inv within `ulps` ulp of
+ * 1 / s (the device takes v_rcp_f32, 1 ulp), t = RN(x * inv) and r = rint(t),
+ * every element whose t is not within 2^-thr of a half-integer must give
+ * r == rint(RN(x / s)), the quotient the reference rounds
+ * (kernels/llama3/quantize.py:142-144). Samples n scales s (normal, in
+ * [2^-100, 2^100], as the kernels' fast path requires) and per scale random
+ * elements |x| <= 7 s plus elements a few ulps from every tie (k + 1/2) s;
+ * each against every inverse from RN(1/s) - ulps to RN(1/s) + ulps ulp.
+ * Returns the number of elements the fast path would round differently (0
+ * for the kernels' threshold, 17; a threshold far too tight shows misses). */
+static uint64_t kvqref_rng(uint64_t* s) {
+  *s ^= *s << 13;
+  *s ^= *s >> 7;
+  *s ^= *s << 17;
+  return *s;
+}
+
+int64_t kvqref_check_rint_margin(uint64_t seed, int64_t n, int ulps, int thr) {
+  int64_t bad = 0;
+  const float margin = 0.5f - ldexpf(1.0f, -thr);
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t st = seed * 0x9E3779B97F4A7C15ull + (uint64_t)i * 0xD1B54A32D192ED03ull + 1;
+    for (int w = 0; w < 4; ++w) kvqref_rng(&st);
+    const int e = (int)(kvqref_rng(&st) % 200) - 100;
+    const float s = ldexpf(1.0f + (float)(kvqref_rng(&st) % 8388608u) / 8388608.0f, e);
+    const float inv0 = 1.0f / s;
+    float xs[64];
+    int nx = 0;
+    for (int j = 0; j < 16; ++j) {  /* random elements in [-7 s, 7 s] */
+      const float u = (float)((double)(kvqref_rng(&st) % 14000001u) / 1000000.0 - 7.0);
+      xs[nx++] = u * s;
+    }
+    for (int k = -8; k <= 6 && nx < 62; k += 2) { /* near the ties (k + 1/2) s */
+      const float tie = ((float)k + 0.5f + (float)(kvqref_rng(&st) % 2)) * s;
+      const int d = (int)(kvqref_rng(&st) % 7) - 3;
+      float x = tie;
+      for (int m = 0; m < (d < 0 ? -d : d); ++m) x = nextafterf(x, d < 0 ? -INFINITY : INFINITY);
+      xs[nx++] = x;
+      xs[nx++] = -x;
+    }
+    for (int q = -ulps; q <= ulps; ++q) {
+      float inv = inv0;
+      for (int m = 0; m < (q < 0 ? -q : q); ++m) inv = nextafterf(inv, q < 0 ? 0.0f : INFINITY);
+      for (int j = 0; j < nx; ++j) {
+        const float x = xs[j];
+        if (fabsf(x) > 7.0f * s) continue;
+        const float t = x * inv;
+        const float r = rintf(t);
+        if (fabsf(t - r) > margin) continue; /* the kernels divide */
+        if (r != rintf(x / s)) ++bad;
+      }
+    }
+  }
+  return bad;
+}

@@ -36,6 +36,8 @@ def lib() -> ctypes.CDLL:
         l.kvqref_num_threads.restype = i32
         l.kvqref_check_div7.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
         l.kvqref_check_div7.restype = i64
+        l.kvqref_check_rint_margin.argtypes = [ctypes.c_uint64, i64, ctypes.c_int, ctypes.c_int]
+        l.kvqref_check_rint_margin.restype = i64
         _lib = l
     return _lib
 

@@ -155,3 +155,19 @@ def test_group_scale_without_division_is_exact():
     zero, all subnormals and all normal values (oracle/kvq_ref.c
     kvqref_check_div7)."""
     assert R.lib().kvqref_check_div7(0, 0x7F800000) == 0
+
+
+def test_rint_with_approximate_inverse_is_exact_outside_the_tie_margin():
+    """The quantize kernels round x / s as rint(RN(x * inv)) with inv =
+    v_rcp_f32(s) (1 ulp), and divide only when RN(x * inv) lies within 2^-17
+    of a half-integer (kv-cache-triton_amd/csrc/kvq_common.h rint_quotient).
+    Sampled scales and elements, random and a few ulps from every tie, with
+    inverses up to 8 ulps off: no element outside the margin rounds
+    differently from rint of the correctly rounded quotient. The same check
+    with a margin below the error bound (2^-20 at 1 ulp, 2^-19 at 2 ulps)
+    finds such elements, so the sampling reaches the ties."""
+    lib = R.lib()
+    assert lib.kvqref_check_rint_margin(11, 4_000_000, 2, 17) == 0
+    assert lib.kvqref_check_rint_margin(12, 1_000_000, 8, 17) == 0
+    assert lib.kvqref_check_rint_margin(13, 1_000_000, 1, 20) > 0
+    assert lib.kvqref_check_rint_margin(13, 1_000_000, 2, 19) > 0
