@@ -89,3 +89,51 @@ def test_pv_weight_rounding_budget_fp16_large_activations():
           f"{e_mbf:.2e}; fp16 output rounding {e_out:.2e}")
     assert e_kernel <= 2e-2
     assert e_kernel <= 1.5 * (e_m16 + e_out)
+
+
+@pytest.mark.parametrize("Sq,Sk,ratio,D", [(2, 50, 4, 128), (4, 300, 1, 64), (16, 100, 4, 128), (8, 1030, 8, 64)])
+def test_fp16_causal_query_blocks(Sq, Sk, ratio, D):
+    """fp16 PV weights in the row-masked kernels (causal query blocks, aligned
+    bottom-right): rows whose keys start inside a tile keep a running max
+    of kNeg until their first key, and their masked keys weigh 0."""
+    print(f"fp16 causal block Sq {Sq} Sk {Sk} ratio {ratio} D {D}", flush=True)
+    Hkv, G = 2, 32
+    g = torch.Generator().manual_seed(Sq * Sk + D)
+    q = torch.randn(1, Hkv * ratio, Sq, D, generator=g).half()
+    kp, ks = ops.quantize(torch.randn(1, Hkv, Sk, D, generator=g).half().to(DEV), G, torch.float16)
+    vp, vs = ops.quantize(torch.randn(1, Hkv, Sk, D, generator=g).half().to(DEV), G, torch.float16)
+    out = ops.fused_decode_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=True,
+                                     sm_scale=D ** -0.5)
+    want = O.attention_over_quantized(q.float().numpy(), kp.cpu().numpy(), ks.float().cpu().numpy(),
+                                      vp.cpu().numpy(), vs.float().cpu().numpy(), group_size=G, is_causal=True)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-2
+
+
+def test_fp16_values_near_the_fp16_limit():
+    """V scales far above 64 take the clamped exponent (E = 30): the weight
+    p * v_scale / 32 stays below 65504 for p <= 32, the fp16 kernels' running
+    max slack. Values up to ~60,000 (scales ~8,600), a peaked and a flat
+    softmax, C5-like ragged batch: within 2e-3 of the output magnitude of the
+    float64 oracle, and finite."""
+    B, H, D, G, L = 4, 25, 64, 32, 600
+    g = torch.Generator().manual_seed(33)
+    lens = torch.randint(64, L + 1, (B,), generator=g)
+    for kmul in (0.1, 3.0):
+        q = torch.randn(B, H, 1, D, generator=g).half()
+        k = (kmul * torch.randn(B, H, L, D, generator=g)).half()
+        v = (15000.0 * torch.randn(B, H, L, D, generator=g)).clamp(-60000, 60000).half()
+        kp, ks = ops.quantize(k.to(DEV), G, torch.float16)
+        vp, vs = ops.quantize(v.to(DEV), G, torch.float16)
+        assert float(vs.float().max()) > 64.0
+        out = ops.fused_decode_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=H, group_size=G,
+                                         is_causal=False, sm_scale=D ** -0.5, seq_lens=lens.to(DEV, torch.int32))
+        got = out.float().cpu().numpy().astype(np.float64)
+        want = O.attention_over_quantized(q.float().numpy(), kp.cpu().numpy(), ks.float().cpu().numpy(),
+                                          vp.cpu().numpy(), vs.float().cpu().numpy(), group_size=G,
+                                          seq_lens=lens.tolist())
+        mag = np.abs(want).max()
+        err = np.abs(got - want).max()
+        print(f"fp16 values near the limit, keys x{kmul}: |out| up to {mag:.0f}, max-abs {err:.3g} "
+              f"({err / mag:.2e} of it)")
+        assert np.isfinite(got).all()
+        assert err <= 2e-3 * mag
