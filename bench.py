@@ -350,7 +350,8 @@ def main() -> int:
         result["roofline"]["ceiling"] = {
             "achieved": best["gbs"], "unit": "GB/s", "frac_of_peak": round(best["gbs"] / HBM_PEAK_GBS, 4),
             "decode_frac_of_ceiling": round(achieved / best["gbs"], 4), "grid": best["grid"],
-            "block": best["block"], "kernel": "stream_read (libkvq_probe.so)",
+            "block": best["block"], "kernarg_preload": best["preload"],
+            "kernel": "stream_read (libkvq_probe.so)",
         }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, layers, attended, seq_lens, args.cpu_seconds)
@@ -417,7 +418,7 @@ def make_layers(w: dict, P: int, dev, stream):
 # workgroup per CU to eight
 PROBE_GRIDS = ((256, 256), (256, 512), (256, 1024), (512, 256), (512, 512), (1024, 256), (1024, 512),
                (2048, 256), (2048, 512))
-CEILING_GRIDS = ((256, 512), (512, 256), (1024, 256), (2048, 256))
+CEILING_GRIDS = ((256, 512), (512, 256), (1024, 256), (2048, 256), (2048, 512))
 
 
 def probe_lib():
@@ -436,9 +437,11 @@ def probe_lib():
         fn = getattr(lib, name)
         fn.restype = getattr(prod, name).restype
         fn.argtypes = getattr(prod, name).argtypes
-    lib.kvq_probe_stream_read.restype = ctypes.c_int
-    lib.kvq_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    for name in ("kvq_probe_stream_read", "kvq_probe_stream_read_preload"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                       ctypes.c_void_p]
     lib.kvq_probe_stream_read_padded.restype = ctypes.c_int
     lib.kvq_probe_stream_read_padded.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                                  ctypes.c_void_p, ctypes.c_void_p]
@@ -450,8 +453,10 @@ def probe_lib():
 def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
     """Streaming read of nbytes (rounded up to 16) from each of L buffers, one
     launch per buffer captured in a HIP graph and replayed 20 times between
-    two events on the launch stream: per (grid, block), the average launch
-    time and GB/s over nbytes."""
+    two events on the launch stream: per (grid, block) and per build of the
+    read (preload False: the wave loads its arguments from memory; True: the
+    hardware preloads them into SGPRs), the average launch time and GB/s over
+    nbytes."""
     import torch
 
     lib = probe_lib()
@@ -460,17 +465,17 @@ def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
     bufs = [torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev, generator=g) for _ in range(L)]
     sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)  # >= any grid below (one word per workgroup)
     out = []
-    for grid, block in grids:
+    for (grid, block), preload in ((gb, pl) for gb in grids for pl in (False, True)):
         # larger buffers: more workgroups, so that each thread keeps at most
         # 20 pieces in flight (no register spills)
         while -(-(n // 16) // (grid * block)) > 20:
             grid *= 2
+        read = lib.kvq_probe_stream_read_preload if preload else lib.kvq_probe_stream_read
         graph = torch.cuda.CUDAGraph()
         per = 0
         with torch.cuda.graph(graph, stream=stream):
             for b in bufs:
-                per = lib.kvq_probe_stream_read(b.data_ptr(), n, grid, block, sink.data_ptr(), None,
-                                                stream.cuda_stream)
+                per = read(b.data_ptr(), n, grid, block, sink.data_ptr(), None, stream.cuda_stream)
         if per <= 0:
             continue
         torch.cuda.synchronize()
@@ -485,8 +490,8 @@ def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
             e1.record(stream)
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / (20 * L)
-        out.append({"grid": grid, "block": block, "pieces_per_thread": per, "us_per_launch": round(us, 3),
-                    "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        out.append({"grid": grid, "block": block, "preload": preload, "pieces_per_thread": per,
+                    "us_per_launch": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
     if keep is not None:
         keep.extend(bufs)
     return out
@@ -533,7 +538,9 @@ def stream_probe_bench(args, w: dict) -> int:
     stream_rows = stream_ceiling(nbytes, L, dev, stream, PROBE_GRIDS, keep)
     best = min(stream_rows, key=lambda r: r["us_per_launch"])
 
-    # per-wave stamps of the read on a cold buffer (the other buffers read first)
+    # per-wave stamps of the read on a cold buffer (the other buffers read first);
+    # the build without argument preload, which starts its waves the way the
+    # decode kernel does
     n = -(-nbytes // 16) * 16
     grid, block = 256, 512
     waves = grid * (block // 64)
@@ -946,10 +953,11 @@ def summarize_probe(path: str) -> str:
     out = [f"streaming read of {d['bytes_per_launch']} B per launch, {d['layers']} buffers, graph of "
            f"{d['layers']} launches x 20 replays:"]
     for r in d["stream"]:
+        pl = "preloaded args" if r.get("preload") else "args from memory"
         out.append(f"  grid {r['grid']:5d} x {r['block']:4d}  {r['pieces_per_thread']:2d} x 16 B per thread  "
-                   f"{r['us_per_launch']:7.3f} us/launch  {r['gbs']:7.1f} GB/s")
+                   f"{pl:<16}  {r['us_per_launch']:7.3f} us/launch  {r['gbs']:7.1f} GB/s")
     for r in d.get("issue_cost", []):
-        out.append(f"  grid   256 x  512  10 x 16 B per thread with {r['valu_instructions']:4d} VALU "
+        out.append(f"  grid   256 x  512  10 x 16 B per thread  args from memory  {r['valu_instructions']:4d} VALU "
                    f"{r['placed']:<12}  {r['us_per_launch']:7.3f} us/launch")
     dec = d["decode_step"]
     out.append(f"decode step (product kernel, same graph timing): {dec['us_per_launch']:.3f} us/launch = "
@@ -966,7 +974,7 @@ def summarize_probe(path: str) -> str:
         return rows
 
     sp = d["stream_phases_ns"]
-    out += table(f"streaming read, per-wave stamps (grid {sp['grid']} x {sp['block']}), ns:", sp,
+    out += table(f"streaming read, per-wave stamps (grid {sp['grid']} x {sp['block']}, args from memory), ns:", sp,
                  ("entry", "loads_issued", "first_arrived", "all_arrived"))
     out += table("decode step, instrumented build (libkvq_probe.so), per wave, ns:", d["decode_phases_ns"],
                  list(d["decode_phases_ns"]))

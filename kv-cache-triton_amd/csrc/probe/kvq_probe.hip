@@ -6,7 +6,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace kvq_probe {
+// Built twice into the library: as is, and with KVQ_PROBE_PRELOAD defined and
+// -amdgpu-kernarg-preload-count, which has the hardware load the kernels'
+// scalar arguments into SGPRs at wave launch. The second build's kernels live
+// in namespace kvq_probe_pl and its entry points carry the suffix _preload.
+// Preload lets a wave issue its loads without first waiting for the argument
+// block to arrive from memory (it helps reads of a few MB and more), but costs
+// the smallest launches a little, so the ceiling takes the best of both.
+#if defined(KVQ_PROBE_PRELOAD)
+#define KVQ_PROBE_NS kvq_probe_pl
+#define KVQ_PROBE_FN(name) name##_preload
+#else
+#define KVQ_PROBE_NS kvq_probe
+#define KVQ_PROBE_FN(name) name
+#endif
+
+namespace KVQ_PROBE_NS {
 
 // Thread t reads the 16-byte pieces t, t + T, ..., t + (PER - 1) T of the
 // buffer (T = threads in the grid; pieces past n16 are skipped), all issued
@@ -124,27 +139,27 @@ static int pieces_per_thread(uint64_t n16, int grid, int block) {
   return 0;
 }
 
-}  // namespace kvq_probe
+}  // namespace KVQ_PROBE_NS
 
 // One streaming read of `bytes` (a multiple of 16) at buf, grid x block
 // threads; sink holds >= grid uint32. stamps (may be null): per-wave clock
 // stamps, [grid * 16 * 4] uint64, block <= 1024. Returns the pieces per
 // thread used, 0 if no instantiation covers the buffer (nothing launched),
 // -1 on bad arguments or a launch error.
-extern "C" int kvq_probe_stream_read(const void* buf, int64_t bytes, int grid, int block, void* sink,
+extern "C" int KVQ_PROBE_FN(kvq_probe_stream_read)(const void* buf, int64_t bytes, int grid, int block, void* sink,
                                      void* stamps, void* stream) {
   if (buf == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || grid <= 0 || block <= 0 ||
       block > 1024 || block % 64 != 0)
     return -1;
   const uint64_t n16 = (uint64_t)bytes / 16;
-  const int per = kvq_probe::pieces_per_thread(n16, grid, block);
+  const int per = KVQ_PROBE_NS::pieces_per_thread(n16, grid, block);
   if (per == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   if (stamps != nullptr)
-    hipLaunchKernelGGL(kvq_probe::pick_stamped(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
+    hipLaunchKernelGGL(KVQ_PROBE_NS::pick_stamped(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
                        (uint32_t*)sink, (uint64_t*)stamps);
   else
-    hipLaunchKernelGGL(kvq_probe::pick(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
+    hipLaunchKernelGGL(KVQ_PROBE_NS::pick(per), dim3(grid), dim3(block), 0, st, (const uint4*)buf, n16,
                        (uint32_t*)sink);
   return hipGetLastError() == hipSuccess ? per : -1;
 }
@@ -153,9 +168,9 @@ extern "C" int kvq_probe_stream_read(const void* buf, int64_t bytes, int grid, i
 // bytes) with grid 256 x 512: pad in {0, 256, 512, 1024, 2048}, after != 0
 // places the instructions after the loads. Returns 0, or -1 on bad arguments
 // or a launch error.
-extern "C" int kvq_probe_stream_read_padded(const void* buf, int64_t bytes, int pad, int after, void* sink,
+extern "C" int KVQ_PROBE_FN(kvq_probe_stream_read_padded)(const void* buf, int64_t bytes, int pad, int after, void* sink,
                                             void* stream) {
-  using namespace kvq_probe;
+  using namespace KVQ_PROBE_NS;
   if (buf == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 != 0 || bytes > 256ll * 512 * 10 * 16) return -1;
   read_fn f = nullptr;
 #define KVQ_PAD_CASE(n)                                                              \
