@@ -156,7 +156,7 @@ __device__ __forceinline__ void phase_stamp(unsigned long long* p, int point) {
 #endif
 
 constexpr float kNeg = -1.0e30f;
-constexpr int kMaxSplit = 64;  // split-K fan-out cap (bounds the merge's LDS)
+constexpr int kMaxSplit = 64;  // split-K fan-out cap (keeps split * L and merge offsets in 32 bits)
 constexpr float kLazyMax = 8.0f;  // running-max slack of the MFMA kernel (log2 units)
 constexpr int kCntStride = 16;  // uint32 words between counters (64 bytes)
 constexpr uint32_t kNibPairs = 0x000F000Fu;
@@ -364,8 +364,6 @@ __device__ __forceinline__ void page_delta(const AttnArgs& a, const int32_t* bt_
   delta = ((uint32_t)blk - pg) << a.page_shift;
 }
 
-constexpr int kMaxRows = 8;  // query rows per workgroup (both kernels)
-
 // Buffer descriptor over `bytes` bytes at p (raw, 32-bit data format): loads
 // at offsets >= bytes return zero and touch no memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
@@ -375,12 +373,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int NT>
+constexpr int kMaxRows = 8;  // query rows per workgroup (both kernels)
+
 struct MergeLds {
-  float4 part_o[NT];           // cross-split merge: per-thread group partials (4 dims)
-  float2 part_ml[NT];          //   and their (max, sum)
   float2 ml[kMaxSplit * kMaxRows];  // the unit's (max, sum) pair of every (split, row)
-  int last;                    // this workgroup merges the unit's splits
+  int last;                         // this workgroup merges the unit's splits
 };
 
 // Partials cross between workgroups of one unit, which all run on one XCD
@@ -400,28 +397,53 @@ __device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_c
 // here are scores, never NaN.
 __device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
+// Reduction over the P lanes l, l + 64 / P, l + 2 * 64 / P, ... of a wave
+// (P in {1, 2, 4, 8, 16}): every one of them ends with their maximum (MAX) or
+// sum. Lane index bits are combined from the top: xor 32 and xor 16 through
+// ds_bpermute (__shfl_xor), xor 8 and xor 4 by rotating 16-lane rows by 8 and
+// then by 4 (a full reduction over a row's residue class modulo 4).
+template <int P, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+  static_assert(P == 1 || P == 2 || P == 4 || P == 8 || P == 16, "group size");
+  auto op = [](float x, float y) { return MAX ? fmax_nc(x, y) : x + y; };
+  if constexpr (P >= 2) v = op(v, __shfl_xor(v, 32));
+  if constexpr (P >= 4) v = op(v, __shfl_xor(v, 16));
+  if constexpr (P >= 8) v = op(v, dpp<0x128>(v, v));  // row_ror:8
+  if constexpr (P >= 16) v = op(v, dpp<0x124>(v, v)); // row_ror:4
+  return v;
+}
+
 // Cross-split merge, run by the last workgroup of a unit to finish: out =
-// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. Thread t
-// owns the 4 dims 4 (t % (D/4)) .. +4 of row (t / (D/4)) % ROWS for the
-// splits congruent to t / (ROWS*D/4) modulo P: it issues all of its 16-byte
-// partial loads for a batch of 8 splits at once and folds them with a running
-// max. The unit's (max, sum) pairs (one per split and row, shared by the
-// threads of a row) are read once, before the output pieces, into LDS; the
-// barrier that publishes them passes while the pieces are still in flight.
-// The P groups of threads sharing a (row, 4 dims) are then combined through
-// LDS. A row no split saw a key for (all l_s = 0) yields zeros.
+// sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s. The
+// unit's partials are Q = ROWS * D / 4 pieces of 16 bytes (4 dims of one row)
+// per split; P = threads / Q threads share a piece. Lane l of wave w takes
+// piece w * 64 / P + l % (64 / P) and, of the splits, those congruent to
+// l / (64 / P) modulo P: the P threads of a piece are lanes 64 / P apart in
+// one wave, and the 64 / P consecutive lanes of one group read consecutive
+// pieces of one split (coalesced). It issues its 16-byte partial loads for a
+// batch of 8 splits at once and folds them with a running max. The unit's
+// (max, sum) pairs (one per split and row, shared by the threads of a row)
+// are read once, before the pieces, into LDS; the barrier that publishes them
+// passes while the pieces are still in flight. The P partial folds of a piece
+// are then combined across lanes (group_reduce: no LDS round trip and no
+// barrier after the last load), and the lanes of group 0 store the 4
+// outputs of their pieces. A row no split saw a key for (all l_s = 0) yields
+// zeros.
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc, int kvh, int b,
-                                             MergeLds<64 * NW>& mg) {
+                                             MergeLds& mg) {
   constexpr int NT = 64 * NW;
   constexpr int Q = ROWS * D / 4;  // 16-byte pieces per split
   static_assert(Q <= NT && NT % Q == 0, "merge mapping");
-  constexpr int P = NT / Q;         // thread groups per piece
+  constexpr int P = NT / Q;         // threads per piece
+  static_assert(64 % P == 0, "a piece's threads lie in one wave");
   constexpr int BATCH = 8;
-  constexpr int MLPT = (kMaxSplit * ROWS + NT - 1) / NT;  // (max, sum) loads per thread
+  constexpr int MLPT = (kMaxSplit * kMaxRows + NT - 1) / NT;  // (max, sum) loads per thread
+  constexpr int PW = 64 / P;       // pieces per wave
   const int tid = threadIdx.x;
   const int ns = a.n_split;
-  const int piece = tid % Q, grp = tid / Q;
+  const int lane = tid & 63;
+  const int piece = (tid >> 6) * PW + lane % PW, grp = lane / PW;
   const int r = piece / (D / 4), d4 = piece % (D / 4);
   const int64_t slot0 = (int64_t)unit * ns * ROWS;  // + split * ROWS + row
   const __amdgpu_buffer_rsrc_t ro =
@@ -432,7 +454,12 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
 #pragma unroll
   for (int k = 0; k < MLPT; ++k)  // index past nml: zeros, not stored below
     mlv[k] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rm, (uint32_t)(tid + k * NT) * 8u, 0, kSc0));
+  // the pairs' loads go out before the pieces' (the compiler would otherwise
+  // place them after): loads complete in issue order, so the LDS store below
+  // then waits for the pairs alone
+  asm volatile("" ::: "memory");
   const int nj = (ns - grp + P - 1) / P;  // splits grp, grp + P, ... < ns
+  const int nj_max = (ns + P - 1) / P;    // the same for grp 0: every lane runs the loop alike
   u32x4_t ov[BATCH];
   auto issue = [&](int j0) {
 #pragma unroll
@@ -451,7 +478,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
   __syncthreads();
   float Mr = kNeg, Lr = 0.0f;
   float4 Or = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int j0 = 0; j0 < nj; j0 += BATCH) {
+  for (int j0 = 0; j0 < nj_max; j0 += BATCH) {
     if (j0 > 0) issue(j0);
     if (j0 == 0) KVQ_STAMP_AFTER(9, ov[BATCH - 1].x);
     // Straight-line fold (no branch per split, so every load above is in
@@ -482,29 +509,17 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
     Mr = mb;
   }
   if constexpr (P > 1) {
-    mg.part_o[tid] = Or;
-    mg.part_ml[tid] = make_float2(Mr, Lr);
-    __syncthreads();
-    if (tid >= Q) return;
-    float M = Mr;
-#pragma unroll
-    for (int g = 1; g < P; ++g) M = fmax_nc(M, mg.part_ml[tid + g * Q].x);
-    const float f0 = __builtin_amdgcn_exp2f(Mr - M);
-    Lr *= f0;
-    Or.x *= f0; Or.y *= f0; Or.z *= f0; Or.w *= f0;
-#pragma unroll
-    for (int g = 1; g < P; ++g) {
-      const float2 ml = mg.part_ml[tid + g * Q];
-      const float4 o = mg.part_o[tid + g * Q];
-      const float f = __builtin_amdgcn_exp2f(ml.x - M);
-      Lr = fmaf(ml.y, f, Lr);
-      Or.x = fmaf(o.x, f, Or.x); Or.y = fmaf(o.y, f, Or.y);
-      Or.z = fmaf(o.z, f, Or.z); Or.w = fmaf(o.w, f, Or.w);
-    }
+    const float M = group_reduce<P, true>(Mr);
+    const float f = __builtin_amdgcn_exp2f(Mr - M);
+    Lr = group_reduce<P, false>(Lr * f);
+    Or.x = group_reduce<P, false>(Or.x * f);
+    Or.y = group_reduce<P, false>(Or.y * f);
+    Or.z = group_reduce<P, false>(Or.z * f);
+    Or.w = group_reduce<P, false>(Or.w * f);
   }
   KVQ_STAMP_AFTER(10, Lr);
   const int rho = rc * ROWS + r;
-  if (rho < a.rows_total) {
+  if (grp == 0 && rho < a.rows_total) {
     const float inv = Lr > 0.0f ? 1.0f / Lr : 0.0f;
     store4_from_f32(a, out_index(a, b, kvh, rho, 4 * d4), OUT_DT, Or.x * inv, Or.y * inv, Or.z * inv, Or.w * inv);
   }
@@ -534,7 +549,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int unit, int rc
 template <int ROWS, int D, int OUT_DT, int NW>
 __device__ __forceinline__ void finish_block(const AttnArgs& a, int unit, int split, int rc,
                                              int kvh, int b, const float (*o_lds)[ROWS][D],
-                                             const float (*ml_lds)[ROWS][2], MergeLds<64 * NW>& mg,
+                                             const float (*ml_lds)[ROWS][2], MergeLds& mg,
                                              const float* nt = nullptr) {
   constexpr int NT = 64 * NW;
   const int tid = threadIdx.x;
@@ -732,7 +747,7 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t q_lds[NW][ROWS][QROW];
   __shared__ __attribute__((aligned(16))) char smem[S_BYTES];
   __shared__ __attribute__((aligned(16))) float ml_lds[NW][ROWS][2];
-  __shared__ MergeLds<64 * NW> mg;
+  __shared__ MergeLds mg;
   // With two row sets, each wave's accumulator init per (row set, chunk),
   // the same in every lane and unchanged by the tile loop, is kept in LDS
   // rather than registers, so that the kernel fits two waves per SIMD. One
@@ -1538,7 +1553,7 @@ __global__ __launch_bounds__(256) void decode_attn_valu_kernel(const AttnArgs a)
   __shared__ __attribute__((aligned(16))) WT w_lds[4][CH][ROWS][LPT][TPT];
   __shared__ float o_lds[4][ROWS][D];
   __shared__ __attribute__((aligned(16))) float ml_lds[4][ROWS][2];
-  __shared__ MergeLds<256> mg;
+  __shared__ MergeLds mg;
   // the decode step's new token: its score per row, then its dequantized
   // values (two elements per lane of the V wave)
   __shared__ __attribute__((aligned(16))) float nt_lds[ROWS + 128];
