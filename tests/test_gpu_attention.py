@@ -272,3 +272,30 @@ def test_fused_attention_random_shapes(seed):
     assert np.isfinite(got).all()
     err = np.abs(got - want).max()
     assert err <= tol, err
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("ratio", [1, 2, 4, 8])
+def test_split_merge_every_group_size(dtype, D, ratio):
+    """The cross-split merge at every lane-group size it has: a piece of the
+    partials (4 dims of one query row) is shared by P = threads / (rows * D /
+    4) threads, lanes 64 / P apart, combined with shuffles: P = 2, 4 or 8 in
+    the matrix kernel (D 64/128, 4 or 8 rows), 1 to 16 in the fp32 kernel (1
+    to 8 rows). Seven splits (not a multiple of any P, so some groups fold
+    fewer splits), ragged lengths, against the float64 oracle."""
+    B, Hkv, Sk = 2, 2, 1500
+    Hq = Hkv * ratio
+    lens = [1500, 700]
+    print(f"merge groups: {dtype} D {D} ratio {ratio}", flush=True)
+    q, kp, ks, vp, vs = _inputs(B, Hq, Hkv, 1, Sk, D, dtype, seed=77 + D + ratio, G=32)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    sm = D ** -0.5
+    out = ops.fused_decode_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=32, is_causal=False,
+                                     sm_scale=sm, seq_lens=sl, n_split=7)
+    got = out.float().cpu().numpy()
+    want = _oracle(q, kp, ks, vp, vs, 32, seq_lens=lens, scale=sm)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    assert np.isfinite(got).all()
+    err = np.abs(got - want).max()
+    assert err <= tol, err
