@@ -212,14 +212,47 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     if (!live[k]) continue;
     const float scale = group_scale(amax);  // amax / 7, correctly rounded
     const float inv = group_inverse(scale);
+    // Codes + 8 without a divide: t = x * inv + 8 in one fma, rounded to an
+    // integer (ties to even) by adding 2^23, so that the sum's low byte is
+    // the code + 8, in [1, 15] for |x| <= 7 s (no clamp). That is rint of
+    // the correctly rounded quotient unless t lies within 2^-17 of a
+    // half-integer (the residual t - rint(t) is exact; the bound is that of
+    // rint_quotient plus the fma's rounding); such elements, and every
+    // element of a group whose scale is outside [2^-100, 2^100], take the
+    // division. One test per row (the residuals' maximum, which propagates
+    // NaN, so a NaN element divides too and gets the division path's code)
+    // keeps the common case free of per-element branches; inside it each
+    // element divides on its own, since with 16-bit inputs exact ties are
+    // common and dividing the whole row cost more than it saved.
+    // oracle/kvq_ref.c kvqref_check_rint_margin_fma8 pins the margin.
     const bool fast = scale >= 0x1p-100f && scale <= 0x1p100f;
-    uint32_t word = 0;
+    uint32_t cb[8];
+    float rmax = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float qf = rint_quotient(x[k][e], scale, inv, fast);  // round half to even
-      qf = fminf(fmaxf(qf, -8.0f), 7.0f);
-      word |= (uint32_t)((int)qf + 8) << (4 * e);
+      const float t = __builtin_fmaf(x[k][e], inv, 8.0f);
+      const float u = t + 0x1p23f;
+      rmax = __builtin_elementwise_maximum(rmax, fabsf(t - (u - 0x1p23f)));
+      cb[e] = __builtin_bit_cast(uint32_t, u);
     }
+    if (!(rmax <= 0.5f - 0x1p-17f && fast)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = __builtin_fmaf(x[k][e], inv, 8.0f);
+        const float u = t + 0x1p23f;
+        if (!(fast && fabsf(t - (u - 0x1p23f)) <= 0.5f - 0x1p-17f)) {
+          const float qf = fminf(fmaxf(__builtin_rintf(x[k][e] / scale), -8.0f), 7.0f);  // round half to even
+          cb[e] = (uint32_t)((int)qf + 8);
+        }
+      }
+    }
+    // byte 0 of cb[e] is element e's code + 8: even elements to the low
+    // nibbles, odd ones to the high nibbles (v_perm_b32 byte gathers)
+    const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(cb[6], cb[4], 0x0c0c0400u),
+                                              __builtin_amdgcn_perm(cb[2], cb[0], 0x0c0c0400u), 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(cb[7], cb[5], 0x0c0c0400u),
+                                              __builtin_amdgcn_perm(cb[3], cb[1], 0x0c0c0400u), 0x05040100u);
+    const uint32_t word = lo | (hi << 4);
     const int64_t b = bb[k], h = hh[k], pos = dst[k];
     if (pos < 0) continue;  // no destination row
     // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)

@@ -301,3 +301,61 @@ int64_t kvqref_check_rint_margin(uint64_t seed, int64_t n, int ulps, int thr) {
   }
   return bad;
 }
+
+/* Pins the packed form of the same rounding in the vector quantize kernel
+ * (quantize_vec_kernel, kv-cache-triton_amd/csrc/kvq_quant.hip): t =
+ * RN(x * inv + 8) in one fma, u = RN(t + 2^23) (t rounded to an integer,
+ * ties to even), c = u - 2^23 and r = t - c (both exact). An element with
+ * |r| <= 1/2 - 2^-thr must have c - 8 == rint(RN(x / s)) and c in [1, 15]
+ * (so no clamp is needed); the kernel divides for the others. Samples as
+ * kvqref_check_rint_margin, plus per scale the group extremes x = +-am for an
+ * absmax am with s = RN(am / 7), the scale the kernels compute. Returns the
+ * number of elements the fast path would get wrong. */
+int64_t kvqref_check_rint_margin_fma8(uint64_t seed, int64_t n, int ulps, int thr) {
+  int64_t bad = 0;
+  const float margin = 0.5f - ldexpf(1.0f, -thr);
+  const float magic = 8388608.0f; /* 2^23 */
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t st = seed * 0x9E3779B97F4A7C15ull + (uint64_t)i * 0xD1B54A32D192ED03ull + 7;
+    for (int w = 0; w < 4; ++w) kvqref_rng(&st);
+    const int e = (int)(kvqref_rng(&st) % 200) - 100;
+    const float am = ldexpf(1.0f + (float)(kvqref_rng(&st) % 8388608u) / 8388608.0f, e);
+    const float s = am / 7.0f;
+    const float inv0 = 1.0f / s;
+    float xs[66];
+    int nx = 0;
+    xs[nx++] = am;
+    xs[nx++] = -am;
+    for (int j = 0; j < 16; ++j) { /* random elements in [-am, am] */
+      const float u = (float)((double)(kvqref_rng(&st) % 14000001u) / 1000000.0 - 7.0);
+      const float x = u * s;
+      xs[nx++] = fabsf(x) <= am ? x : (x < 0 ? -am : am);
+    }
+    for (int k = -8; k <= 6 && nx < 64; k += 2) { /* near the ties (k + 1/2) s */
+      const float tie = ((float)k + 0.5f + (float)(kvqref_rng(&st) % 2)) * s;
+      const int d = (int)(kvqref_rng(&st) % 7) - 3;
+      float x = tie;
+      for (int m = 0; m < (d < 0 ? -d : d); ++m) x = nextafterf(x, d < 0 ? -INFINITY : INFINITY);
+      xs[nx++] = x;
+      xs[nx++] = -x;
+    }
+    for (int q = -ulps; q <= ulps; ++q) {
+      float inv = inv0;
+      for (int m = 0; m < (q < 0 ? -q : q); ++m) inv = nextafterf(inv, q < 0 ? 0.0f : INFINITY);
+      for (int j = 0; j < nx; ++j) {
+        const float x = xs[j];
+        if (fabsf(x) > am) continue;
+        const float t = fmaf(x, inv, 8.0f);
+        const float u = t + magic;
+        const float c = u - magic;
+        const float r = t - c;
+        if (fabsf(r) > margin) continue; /* the kernel divides */
+        float ref = rintf(x / s);
+        ref = fminf(fmaxf(ref, -8.0f), 7.0f);
+        if (c - 8.0f != ref || c < 1.0f || c > 15.0f) ++bad;
+      }
+    }
+  }
+  return bad;
+}

@@ -38,6 +38,8 @@ def lib() -> ctypes.CDLL:
         l.kvqref_check_div7.restype = i64
         l.kvqref_check_rint_margin.argtypes = [ctypes.c_uint64, i64, ctypes.c_int, ctypes.c_int]
         l.kvqref_check_rint_margin.restype = i64
+        l.kvqref_check_rint_margin_fma8.argtypes = [ctypes.c_uint64, i64, ctypes.c_int, ctypes.c_int]
+        l.kvqref_check_rint_margin_fma8.restype = i64
         _lib = l
     return _lib
 

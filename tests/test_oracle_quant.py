@@ -171,3 +171,20 @@ def test_rint_with_approximate_inverse_is_exact_outside_the_tie_margin():
     assert lib.kvqref_check_rint_margin(12, 1_000_000, 8, 17) == 0
     assert lib.kvqref_check_rint_margin(13, 1_000_000, 1, 20) > 0
     assert lib.kvqref_check_rint_margin(13, 1_000_000, 2, 19) > 0
+
+
+def test_packed_rint_with_magic_add_is_exact_outside_the_tie_margin():
+    """The vector quantize kernel computes code + 8 as u - 2^23 with
+    u = RN(RN(x * inv + 8) + 2^23) (one fma, one add that rounds to an
+    integer, ties to even), and divides only when the exact residual
+    t - (u - 2^23) is within 2^-17 of 1/2
+    (kv-cache-triton_amd/csrc/kvq_quant.hip quantize_vec_kernel). Sampled as
+    above, plus the group extremes +-absmax with s = RN(absmax / 7): every
+    element outside the margin gets rint of the correctly rounded quotient,
+    and a code in [1, 15] (so the kernel needs no clamp there). A margin
+    below the error bound finds misses, so the sampling reaches the ties."""
+    lib = R.lib()
+    assert lib.kvqref_check_rint_margin_fma8(11, 4_000_000, 2, 17) == 0
+    assert lib.kvqref_check_rint_margin_fma8(12, 1_000_000, 8, 17) == 0
+    assert lib.kvqref_check_rint_margin_fma8(13, 1_000_000, 1, 20) > 0
+    assert lib.kvqref_check_rint_margin_fma8(13, 1_000_000, 2, 20) > 0
