@@ -979,12 +979,17 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
       r0 = 0;
     }
     svr[i] = load_scales(tvs, (r0 + lane) * vss2);
+    // token s * SUB + VTS * k + vts, dword vj: the lane's part of the offset
+    // once per tile, plus a wave-uniform row offset per load (one add each,
+    // not a 32 x 32-bit multiply-add; the whole offset stays in the vector
+    // operand, so the buffer's range check sees it)
+    const uint32_t vbase = (r0 + (uint32_t)vts) * vps + 4u * (uint32_t)vj;
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint32_t j = (uint32_t)(s * SUB + VTS * k + vts);
-        vq[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(tv, (r0 + j) * vps + 4u * (uint32_t)vj, 0, 0);
+        const uint32_t du = __builtin_amdgcn_readfirstlane((uint32_t)(s * SUB + VTS * k) * vps);
+        vq[i][s][k] = __builtin_amdgcn_raw_buffer_load_b32(tv, vbase + du, 0, 0);
       }
   };
 
