@@ -215,3 +215,69 @@ def test_quantize_random_shapes(seed):
     out = ops.dequantize(packed, scales, G, D, torch.float32)
     want = O.dequantize_int4(packed.cpu().numpy(), _np(scales), G, D, "f32")
     assert np.array_equal(_np(out), want)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_non_finite_and_extreme_groups_agree_across_kernels(dtype):
+    """Groups with a NaN element, +-inf, all zeros, values near the format's
+    largest and smallest normals (scales outside [2^-100, 2^100], where the
+    kernels divide for every element): the vector quantize kernel, the
+    general one (taken for a strided input) and the decode step's in-kernel
+    append write the same bytes. The reference defines no codes for
+    non-finite inputs (its fp32 division and round give NaN before the int
+    cast), so this pins the three HIP paths to each other; the finite groups
+    of the same rows are also checked against the oracle."""
+    B, H, D, G = 2, 4, 128, 32
+    tdt = TDT[dtype]
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(B, H, 1, D, generator=g) * 2).to(tdt)
+    big = 3.0e38 if dtype == "bf16" else 6.0e4
+    tiny = 2.0e-38 if dtype == "bf16" else 7.0e-5
+    x[0, 0, 0, 3] = float("nan")
+    x[0, 1, 0, 40] = float("inf")
+    x[1, 2, 0, 70] = float("-inf")
+    x[1, 3, 0, 96:128] = 0
+    x[0, 2, 0, 0:32] = torch.linspace(-big, big, 32).to(tdt)
+    x[1, 0, 0, 32:64] = torch.linspace(-tiny, tiny, 32).to(tdt)
+    xd = x.to(DEV)
+    special = {(0, 0, 0), (0, 1, 1), (1, 2, 2), (0, 2, 0), (1, 0, 1)}  # (b, h, group) with non-finite / extreme values
+
+    kp_a = torch.zeros(B, H, 4, D // 2, dtype=torch.uint8, device=DEV)
+    ks_a = torch.zeros(B, H, 4, D // G, dtype=tdt, device=DEV)
+    ops.quantize_into(xd, kp_a, ks_a, G, 0)  # contiguous rows: the vector kernel
+    xs = torch.zeros(B, H, 1, 2 * D, dtype=tdt, device=DEV)
+    xs[..., ::2] = xd
+    kp_b = torch.zeros_like(kp_a)
+    ks_b = torch.zeros_like(ks_a)
+    ops.quantize_into(xs[..., ::2], kp_b, ks_b, G, 0)  # element stride 2: the general kernel
+    kp_c, vp_c = torch.zeros_like(kp_a), torch.zeros_like(kp_a)
+    ks_c, vs_c = torch.zeros_like(ks_a), torch.zeros_like(ks_a)
+    q = torch.randn(B, H, 1, D, generator=g).to(tdt).to(DEV)
+    ops.decode_step(q, xd, xd, kp_c, ks_c, vp_c, vs_c, 0, n_kv_heads=H, group_size=G, sm_scale=D ** -0.5)
+    torch.cuda.synchronize()
+    row = lambda t: t[:, :, 0].cpu()
+    bits = lambda t: row(t).view(torch.int16)
+    assert torch.equal(row(kp_a), row(kp_b)) and torch.equal(bits(ks_a), bits(ks_b))
+    assert torch.equal(row(kp_a), row(kp_c)) and torch.equal(bits(ks_a), bits(ks_c))
+    assert torch.equal(row(kp_a), row(vp_c)) and torch.equal(bits(ks_a), bits(vs_c))
+    # a NaN element codes as -8 (byte nibble 0) in a group whose scale the
+    # finite elements set; +-inf gives an infinite scale, NaN quotients, code 0
+    # for the inf element and 8 for the finite ones (x / inf = 0)
+    codes = row(kp_a).numpy()
+    nib = lambda b, h, d: (codes[b, h, d // 2] >> (4 * (d % 2))) & 15
+    assert nib(0, 0, 3) == 0
+    assert nib(0, 1, 40) == 0 and nib(0, 1, 41) == 8
+    assert nib(1, 3, 100) == 8  # an all-zero group: scale 1, codes 8
+    # the finite groups against the oracle
+    with np.errstate(invalid="ignore"):  # the special groups' NaN quotients (not compared)
+        want_p, want_s = O.quantize_int4(x.float().numpy(), G, dtype)
+    got_s = O.bits(_np(ks_a[:, :, :1]), dtype)
+    want_sb = O.bits(want_s, dtype)
+    for b in range(B):
+        for h in range(H):
+            for grp in range(D // G):
+                if (b, h, grp) in special:
+                    continue
+                sl = slice(grp * G // 2, (grp + 1) * G // 2)
+                assert np.array_equal(codes[b, h, sl], want_p[b, h, 0, sl]), (b, h, grp)
+                assert got_s[b, h, 0, grp] == want_sb[b, h, 0, grp], (b, h, grp)
