@@ -43,7 +43,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kRows = 64;    // query rows per workgroup (4 waves x 16)
+constexpr int kWaveRows = 16;  // query rows per wave and row block
 constexpr int kKeys = 64;    // keys per tile
 constexpr float kNegP = -1.0e30f;
 // Running-max slack (log2 units): a row's reference max moves, and its state
@@ -117,10 +117,9 @@ __device__ __forceinline__ float scale_f32(uint32_t bits) {
 // The tile's share of one thread dequantized as (n - 8) sc directly (the
 // rare tiles with a scale beyond 2^125, where -8 sc would overflow): K code
 // dwords k (D / 32 of them used), V code words v (one per key), raw scales.
-template <int D, bool F16, bool S_F16, int KP, int VP>
+template <int D, bool F16, bool S_F16, int KP, int VP, int KB, int VD>
 __device__ __attribute__((noinline)) void store_tile_direct(uint16_t* k_dst, uint16_t* v_dst, uint4 k,
                                                             uint32_t ksc, uint4 v, uint4 vsc) {
-  constexpr int KB = D / 8, VD = D / 16;
   const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
   const float ksf = scale_f32<S_F16>(ksc);
 #pragma unroll
@@ -149,11 +148,15 @@ __device__ __attribute__((noinline)) void store_tile_direct(uint16_t* k_dst, uin
 // RB = 16-row blocks per wave (1 or 2): with two, every K and V fragment read
 // from LDS feeds two MFMAs, halving LDS traffic and dequantize work per row.
 // Two row blocks per wave must stay within 256 registers (two waves per
-// SIMD, two workgroups per CU): one more register halves the occupancy.
-template <int D, bool F16, bool S_F16, int RB, bool PAGED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RB == 2 ? 2 : 1)))
+// SIMD): one more register halves the occupancy. NW = waves per workgroup
+// (4, or 8 for D = 128 with two row blocks): the workgroup's threads share
+// the dequantize of each K/V tile, so eight waves (one workgroup per CU
+// instead of two of four) halve its VALU per wave.
+template <int D, bool F16, bool S_F16, int RB, bool PAGED, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(RB == 2 ? 2 : 1)))
 void prefill_attn_kernel(const PrefillArgs a) {
-  constexpr int ROWS = kRows * RB;  // query rows per workgroup
+  constexpr int NT = 64 * NW;
+  constexpr int ROWS = kWaveRows * NW * RB;  // query rows per workgroup
   constexpr int KP = D + 8;      // K tile row pitch in LDS (elements)
   constexpr int VP = kKeys + 8;  // V^T tile row pitch
   constexpr int NK = D / 32;     // 32-dim steps of S^T
@@ -250,15 +253,18 @@ void prefill_attn_kernel(const PrefillArgs a) {
   const __amdgpu_buffer_rsrc_t rvs = prefill_rsrc(vs_bh, Sk * vss2);
   const int32_t* bt_b = PAGED ? a.bt + (int64_t)b * a.bt_stride : nullptr;
 
-  // tile loaders. K: thread (key tid / 4, quarter tid % 4) takes D / 4 dims
-  // (D / 8 code bytes, one scale group). V: thread (keys 4 (tid % 16) .. + 3,
-  // dims (tid / 16) * D / 16 .. + D / 16) so that it writes V^T rows of four
-  // consecutive keys.
-  constexpr int KB = D / 8;    // K code bytes per thread
-  constexpr int VD = D / 16;   // V dims per thread
-  const int k_key = tid >> 2, k_q = tid & 3;
+  // tile loaders. K: thread (key tid / KQ, part tid % KQ) takes D / KQ dims
+  // (KB = D / (2 KQ) code bytes, within one scale group). V: thread (keys
+  // 4 (tid % 16) .. + 3, dims (tid / 16) VD .. + VD) so that it writes V^T
+  // rows of four consecutive keys.
+  constexpr int KQ = NT / 64;          // threads per key row
+  constexpr int KB = D / (2 * KQ);     // K code bytes per thread
+  constexpr int VD = D / (NT / 16);    // V dims per thread
+  static_assert(KB == 16 || KB == 8 || KB == 4, "K loader width");
+  static_assert(VD == 8 || VD == 4, "V loader width");
+  const int k_key = tid / KQ, k_q = tid % KQ;
   const int v_kq = tid & 15, v_dq = tid >> 4;
-  const uint32_t k_grp = (uint32_t)((k_q * (D / 4)) / a.G);
+  const uint32_t k_grp = (uint32_t)((k_q * (2 * KB)) / a.G);
   const uint32_t v_grp = (uint32_t)((v_dq * VD) / a.G);
   uint32_t kraw[KB / 4];
   uint32_t ksc;
@@ -287,9 +293,11 @@ void prefill_attn_kernel(const PrefillArgs a) {
     if constexpr (KB == 16) {
       const u32x4_t w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(tk, kr * kps + 16u * k_q, 0, 0));
       kraw[0] = w.x; kraw[1] = w.y; kraw[2] = w.z; kraw[3] = w.w;
-    } else {
+    } else if constexpr (KB == 8) {
       const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(tk, kr * kps + 8u * k_q, 0, 0));
       kraw[0] = w.x; kraw[1] = w.y;
+    } else {
+      kraw[0] = __builtin_amdgcn_raw_buffer_load_b32(tk, kr * kps + 4u * k_q, 0, 0);
     }
     ksc = __builtin_amdgcn_raw_buffer_load_b16(tks, kr * kss2 + 2u * k_grp, 0, 0);
 #pragma unroll
@@ -310,7 +318,7 @@ void prefill_attn_kernel(const PrefillArgs a) {
   // its own (inlined, a second copy of the tile code in the loop doubles the
   // registers the compiler holds across it).
   auto store_tile = [&](int buf) {
-    uint16_t* k_dst = k_lds[buf] + k_key * KP + k_q * (D / 4);
+    uint16_t* k_dst = k_lds[buf] + k_key * KP + k_q * (2 * KB);
     uint16_t* v_dst = v_lds[buf] + (v_dq * VD) * VP + 4 * v_kq;
     const float ksf = scale_f32<S_F16>(ksc);
     bool wide = !(fabsf(ksf) <= 0x1p125f);
@@ -351,8 +359,9 @@ void prefill_attn_kernel(const PrefillArgs a) {
         *(uint2*)(v_dst + d * VP) = make_uint2(pack2<F16>(vf[0][d], vf[1][d]), pack2<F16>(vf[2][d], vf[3][d]));
     }
     if (__builtin_amdgcn_ballot_w64(wide) != 0)
-      store_tile_direct<D, F16, S_F16, KP, VP>(k_dst, v_dst, make_uint4(kraw[0], kraw[1], kraw[KB / 4 > 2 ? 2 : 0],
-                                                                        kraw[KB / 4 > 2 ? 3 : 1]),
+      store_tile_direct<D, F16, S_F16, KP, VP, KB, VD>(k_dst, v_dst,
+                                                       make_uint4(kraw[0], kraw[KB / 4 > 1 ? 1 : 0],
+                                                                  kraw[KB / 4 > 2 ? 2 : 0], kraw[KB / 4 > 2 ? 3 : 0]),
                                                ksc, make_uint4(vraw[0], vraw[1], vraw[2], vraw[3]),
                                                make_uint4(vsc[0], vsc[1], vsc[2], vsc[3]));
   };
@@ -482,7 +491,7 @@ void prefill_attn_kernel(const PrefillArgs a) {
     float l_tot = l_run[r] + __shfl_xor(l_run[r], 16);
     l_tot += __shfl_xor(l_tot, 32);
     if (a.n_split > 1) {  // partial of this split, merged by prefill_merge_kernel
-      const int rr = wave * 16 * RB + 16 * r + lq;
+      const int rr = wave * kWaveRows * RB + 16 * r + lq;
       const int64_t slot = ((((int64_t)b * a.row_blocks + blk) * a.Hkv + kvh) * a.n_split + sp) * ROWS + rr;
       float* po = a.ws_o + slot * D;
 #pragma unroll
@@ -538,45 +547,58 @@ __global__ __launch_bounds__(D) void prefill_merge_kernel(const PrefillArgs a, i
   orow[d] = F16 ? (uint16_t)f32_to_f16_bits(v) : (uint16_t)f32_to_bf16_bits(v);
 }
 
-template <int D, bool F16, int RB>
+template <int D, bool F16, int RB, int NW>
 void launch_prefill(const PrefillArgs& a, bool s_f16, dim3 grid, hipStream_t st) {
+  const dim3 block(64 * NW);
   if (a.bt) {
-    if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB, true>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB, true>), grid, dim3(256), 0, st, a);
+    if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB, true, NW>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB, true, NW>), grid, block, 0, st, a);
   } else {
-    if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB, false>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB, false>), grid, dim3(256), 0, st, a);
+    if (s_f16) hipLaunchKernelGGL((prefill_attn_kernel<D, F16, true, RB, false, NW>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_attn_kernel<D, F16, false, RB, false, NW>), grid, block, 0, st, a);
   }
 }
 
 template <int D, bool F16>
-void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, dim3 grid, hipStream_t st) {
-  if (rb == 2) launch_prefill<D, F16, 2>(a, s_f16, grid, st);
-  else launch_prefill<D, F16, 1>(a, s_f16, grid, st);
+void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, int nw, dim3 grid, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (nw == 8) launch_prefill<D, F16, 2, 8>(a, s_f16, grid, st);
+    else if (rb == 2) launch_prefill<D, F16, 2, 4>(a, s_f16, grid, st);
+    else launch_prefill<D, F16, 1, 4>(a, s_f16, grid, st);
+  } else {
+    if (rb == 2) launch_prefill<D, F16, 2, 4>(a, s_f16, grid, st);
+    else launch_prefill<D, F16, 1, 4>(a, s_f16, grid, st);
+  }
   if (a.n_split > 1) {
-    const int rows = kRows * rb;
+    const int rows = kWaveRows * nw * rb;
     const int64_t n = (int64_t)grid.x / a.n_split * rows;
     hipLaunchKernelGGL((prefill_merge_kernel<D, F16>), dim3((unsigned)n), dim3(D), 0, st, a, rows);
   }
 }
 
-// Launch plan: rows per workgroup (rb 16-row blocks per wave), row blocks,
-// and the split over keys. Two row blocks per wave once that still gives a
-// workgroup per CU of a 256-CU device; below 512 workgroups (two per CU),
-// splits of at least 512 keys bring the launch to ~512.
+// Launch plan: waves per workgroup (nw), rows per workgroup (nw waves of rb
+// 16-row blocks), row blocks, and the split over keys. Two row blocks per
+// wave once that still gives a workgroup of four waves per CU of a 256-CU
+// device. D = 128 with two row blocks takes eight waves per workgroup (one
+// workgroup of 256 rows per CU) once that gives at least two rounds of 256
+// workgroups. Below 512 workgroups of four waves (two per CU), splits of at
+// least 512 keys bring the launch to ~512.
 struct PrefillPlan {
-  int rb, n_split;
+  int rb, nw, n_split;
   int64_t row_blocks;
 };
 
-PrefillPlan prefill_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk) {
+PrefillPlan prefill_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
   const int64_t ratio = Hq / Hkv;
+  const int64_t rows = Sq * ratio;
   PrefillPlan p;
-  p.rb = B * Hkv * ((Sq * ratio + 2 * kRows - 1) / (2 * kRows)) >= 256 ? 2 : 1;
-  p.row_blocks = (Sq * ratio + p.rb * kRows - 1) / (p.rb * kRows);
+  p.rb = B * Hkv * ((rows + 8 * kWaveRows - 1) / (8 * kWaveRows)) >= 256 ? 2 : 1;
+  p.nw = (D == 128 && p.rb == 2 && B * Hkv * ((rows + 16 * kWaveRows - 1) / (16 * kWaveRows)) >= 512) ? 8 : 4;
+  const int64_t wg_rows = kWaveRows * p.nw * p.rb;
+  p.row_blocks = (rows + wg_rows - 1) / wg_rows;
   const int64_t n_wg = B * Hkv * p.row_blocks;
   int64_t ns = 1;
-  if (n_wg > 0 && n_wg < 512) {
+  if (p.nw == 4 && n_wg > 0 && n_wg < 512) {
     ns = (512 + n_wg - 1) / n_wg;
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, Sk / 512));
     ns = std::min<int64_t>(ns, 64);
@@ -587,7 +609,7 @@ PrefillPlan prefill_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t
 
 int64_t prefill_ws_bytes(const PrefillPlan& p, int64_t B, int64_t Hkv, int64_t D) {
   if (p.n_split <= 1) return 0;
-  return B * Hkv * p.row_blocks * p.n_split * (kRows * p.rb) * (D + 2) * 4;
+  return B * Hkv * p.row_blocks * p.n_split * (kWaveRows * p.nw * p.rb) * (D + 2) * 4;
 }
 
 }  // namespace
@@ -654,7 +676,7 @@ int prefill_impl(const void* q, int q_dtype, const int64_t* q_strides, const voi
   if (B == 0 || Sq == 0) return KVQ_OK;
   KVQ_CHECK_ARG(q && out && (Sk == 0 || (k_packed && k_scales && v_packed && v_scales)),
                 "kvq_prefill_attn: null data pointer");
-  PrefillPlan plan = prefill_plan(B, Hq, Hkv, Sq, Sk);
+  PrefillPlan plan = prefill_plan(B, Hq, Hkv, Sq, Sk, D);
   // the split over keys needs the workspace; without one the launch is unsplit
   const int64_t need = prefill_ws_bytes(plan, B, Hkv, D);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) plan.n_split = 1;
@@ -688,17 +710,18 @@ int prefill_impl(const void* q, int q_dtype, const int64_t* q_strides, const voi
   if (pg && pg->bt_cols == 0) a.Sk = 0;
   a.n_split = plan.n_split;
   a.ws_o = plan.n_split > 1 ? (float*)workspace : nullptr;
-  a.ws_ml = plan.n_split > 1 ? (float*)workspace + B * Hkv * row_blocks * plan.n_split * (kRows * rb) * D : nullptr;
+  a.ws_ml = plan.n_split > 1 ? (float*)workspace + B * Hkv * row_blocks * plan.n_split * (kWaveRows * plan.nw * rb) * D
+                              : nullptr;
 
   const dim3 grid((unsigned)n_wg);
   hipStream_t st = (hipStream_t)stream;
   const bool f16 = q_dtype == KVQ_F16, s_f16 = scale_dtype == KVQ_F16;
   if (D == 128) {
-    if (f16) launch_prefill_rb<128, true>(a, s_f16, rb, grid, st);
-    else launch_prefill_rb<128, false>(a, s_f16, rb, grid, st);
+    if (f16) launch_prefill_rb<128, true>(a, s_f16, rb, plan.nw, grid, st);
+    else launch_prefill_rb<128, false>(a, s_f16, rb, plan.nw, grid, st);
   } else {
-    if (f16) launch_prefill_rb<64, true>(a, s_f16, rb, grid, st);
-    else launch_prefill_rb<64, false>(a, s_f16, rb, grid, st);
+    if (f16) launch_prefill_rb<64, true>(a, s_f16, rb, plan.nw, grid, st);
+    else launch_prefill_rb<64, false>(a, s_f16, rb, plan.nw, grid, st);
   }
   KVQ_CHECK_LAUNCH("kvq_prefill_attn");
   return KVQ_OK;
@@ -731,7 +754,7 @@ extern "C" int64_t kvq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64
     return KVQ_EINVAL;
   }
   if (B == 0 || Sq == 0) return 0;
-  return prefill_ws_bytes(prefill_plan(B, Hq, Hkv, Sq, Sk), B, Hkv, D);
+  return prefill_ws_bytes(prefill_plan(B, Hq, Hkv, Sq, Sk, D), B, Hkv, D);
 }
 
 extern "C" int kvq_prefill_attn_paged(const void* q, int q_dtype, const int64_t* q_strides,

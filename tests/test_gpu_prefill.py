@@ -115,6 +115,30 @@ def test_prefill_two_row_blocks_per_wave(B):
         assert np.abs(got[:, :, i:i + 1] - want).max() <= 2e-2, i
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_prefill_eight_waves_per_workgroup(dtype):
+    """D = 128 launches of at least 512 workgroups of 256 rows take eight
+    waves per workgroup (each thread dequantizes half as much of a K/V tile):
+    here 8 KV heads x 4096 query positions x GQA 4. The whole output against
+    the dense route, and rows across the block (including the first and last
+    of a workgroup and of its waves) against the fp64 oracle."""
+    Hq, Hkv, Sq, Sk, D, G = 32, 8, 4096, 4160, 128, 32
+    assert Hkv * (Sq * (Hq // Hkv) // 256) >= 512
+    q, kp, ks, vp, vs = _inputs(1, Hq, Hkv, Sq, Sk, D, dtype, G, seed=23)
+    out = ops.prefill_attention(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G, is_causal=True,
+                                sm_scale=D ** -0.5)
+    dense = ops.dense_attention_over_quantized(q.to(DEV), kp, ks, vp, vs, n_kv_heads=Hkv, group_size=G,
+                                               is_causal=True, sm_scale=D ** -0.5)
+    assert (out.float() - dense.float()).abs().max().item() <= 2e-2
+    got = out.float().cpu().numpy()
+    for i in (0, 1, 7, 8, 63, 64, 2047, 4095):
+        n = Sk - Sq + i + 1
+        want = O.attention_over_quantized(
+            q[:, :, i:i + 1].float().numpy(), kp[:, :, :n].cpu().numpy(), ks[:, :, :n].float().cpu().numpy(),
+            vp[:, :, :n].cpu().numpy(), vs[:, :, :n].float().cpu().numpy(), group_size=G, is_causal=False)
+        assert np.abs(got[:, :, i:i + 1] - want).max() <= 2e-2, i
+
+
 def _random_prefill_case(seed):
     r = np.random.default_rng(6000 + seed)
     dtype = ["bf16", "f16"][r.integers(2)]
