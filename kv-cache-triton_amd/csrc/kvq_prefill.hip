@@ -580,9 +580,9 @@ void launch_prefill_rb(const PrefillArgs& a, bool s_f16, int rb, int nw, dim3 gr
 // 16-row blocks), row blocks, and the split over keys. Two row blocks per
 // wave once that still gives a workgroup of four waves per CU of a 256-CU
 // device. D = 128 with two row blocks takes eight waves per workgroup (one
-// workgroup of 256 rows per CU) once that gives at least two rounds of 256
-// workgroups. Below 512 workgroups of four waves (two per CU), splits of at
-// least 512 keys bring the launch to ~512.
+// workgroup of 256 rows per CU) once that still gives a workgroup per CU.
+// Below 512 workgroups of four waves (two per CU), splits of at least 512
+// keys bring the launch to ~512.
 struct PrefillPlan {
   int rb, nw, n_split;
   int64_t row_blocks;
@@ -593,7 +593,7 @@ PrefillPlan prefill_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t
   const int64_t rows = Sq * ratio;
   PrefillPlan p;
   p.rb = B * Hkv * ((rows + 8 * kWaveRows - 1) / (8 * kWaveRows)) >= 256 ? 2 : 1;
-  p.nw = (D == 128 && p.rb == 2 && B * Hkv * ((rows + 16 * kWaveRows - 1) / (16 * kWaveRows)) >= 512) ? 8 : 4;
+  p.nw = (D == 128 && p.rb == 2 && B * Hkv * ((rows + 16 * kWaveRows - 1) / (16 * kWaveRows)) >= 256) ? 8 : 4;
   const int64_t wg_rows = kWaveRows * p.nw * p.rb;
   p.row_blocks = (rows + wg_rows - 1) / wg_rows;
   const int64_t n_wg = B * Hkv * p.row_blocks;

@@ -94,7 +94,8 @@ def test_prefill_empty_cache_and_unsupported():
 @pytest.mark.parametrize("B", [1, 2])
 def test_prefill_two_row_blocks_per_wave(B):
     """Launches of >= 256 workgroups of 128 rows take two 16-row blocks per
-    wave (B = 2: 512 of them, unsplit; B = 1: 256, split in two over keys):
+    wave (B = 2: 256 workgroups of eight waves and 256 rows, unsplit; B = 1:
+    256 of four waves and 128 rows, split in two over keys):
     the whole output against the dense route, and rows across the block
     against the fp64 oracle (row i of a causal block after cached tokens
     attends keys [0, Sk - Sq + i])."""
@@ -117,9 +118,9 @@ def test_prefill_two_row_blocks_per_wave(B):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_prefill_eight_waves_per_workgroup(dtype):
-    """D = 128 launches of at least 512 workgroups of 256 rows take eight
+    """D = 128 launches of at least 256 workgroups of 256 rows take eight
     waves per workgroup (each thread dequantizes half as much of a K/V tile):
-    here 8 KV heads x 4096 query positions x GQA 4. The whole output against
+    here 8 KV heads x 4096 query positions x GQA 4 (512). The whole output against
     the dense route, and rows across the block (including the first and last
     of a workgroup and of its waves) against the fp64 oracle."""
     Hq, Hkv, Sq, Sk, D, G = 32, 8, 4096, 4160, 128, 32
