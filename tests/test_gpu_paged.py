@@ -376,8 +376,9 @@ def test_paged_attend_small_pages_use_dense_route():
                                              (1, 8, 2, 100, 2000, 64)])
 def test_prefill_kernel_paged_matches_contiguous(B, Hq, Hkv, Sq, S, P):
     """The matrix-core prefill kernel through a block table (one and two row
-    blocks per wave) reads the same keys in the same 64-key tiles as on the
-    contiguous cache: bit-identical outputs."""
+    blocks per wave; the second case takes eight waves per workgroup) reads
+    the same keys in the same 64-key tiles as on the contiguous cache:
+    bit-identical outputs."""
     D, G = 128, 32
     lens = [S] * B
     n_blocks = sum(-(-n // P) for n in lens) + 3
