@@ -1,6 +1,7 @@
 """Benchmark of the INT4-KV decode path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--workload ns|c2|c4|c5|c1] [--no-cpu-baseline]
+    python bench.py --prefill SQ | --quantize | --model | --stream-probe   (other lines)
 
 A step is one decode token through every layer of the workload: per layer,
 quantize-append the new token's K and V into that layer's INT4 cache (in
@@ -89,6 +90,8 @@ def main() -> int:
     ap.add_argument("--prefill", type=int, default=0, metavar="SQ",
                     help="time the matrix-core prefill kernel instead: a causal block of SQ query tokens "
                          "over the workload's context (SQ == --ctx: a whole prompt), one JSON line")
+    ap.add_argument("--quantize", action="store_true",
+                    help="time kvq_quantize / kvq_dequantize on a prompt append of the workload's shape")
     ap.add_argument("--model", action="store_true",
                     help="whole-model decode instead: random-init Llama-3.1-8B (C3), 16K prompt, 64 greedy "
                          "steps over the INT4 cache, each step one HIP graph replay")
@@ -158,6 +161,8 @@ def main() -> int:
         w["ctx"] = args.ctx
     if args.prefill:
         return prefill_bench(args, w)
+    if args.quantize:
+        return quantize_bench(args, w)
     if args.model:
         return model_bench(args)
     if args.stream_probe:
@@ -764,6 +769,110 @@ def prefill_bench(args, w: dict) -> int:
     return 0
 
 
+def quantize_bench(args, w: dict) -> int:
+    """The quantizer on a prompt append: x [B, Hkv, ctx, D] of the workload's
+    activation dtype quantized into fresh cache tensors (`kvq_quantize`, the
+    path's a1 row), and the same codes dequantized back (`kvq_dequantize`).
+    Bytes per launch: the input read plus codes and scales written (quantize),
+    codes and scales read plus the output written (dequantize). Enough
+    buffers rotate that one round exceeds the 256 MB Infinity Cache; the
+    launches are captured in a HIP graph and timed with events on the launch
+    stream."""
+    import math
+
+    import torch
+
+    from kvint4 import ops
+
+    B, Hkv, D, G, S = w["B"], w["Hkv"], w["D"], w["G"], w["ctx"]
+    if w["dtype"] == "f32":
+        print("bench.py: --quantize takes a 16-bit workload", file=sys.stderr)
+        return 2
+    dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float16
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    W_, NG = ops.packed_width(D, G), ops.num_groups(D, G)
+    n = B * Hkv * S
+    x_bytes, code_bytes = n * D * 2, n * (W_ + 2 * NG)
+    nbuf = max(2, math.ceil((512 << 20) / (x_bytes + code_bytes)))
+    gen = torch.Generator(device=dev).manual_seed(5)
+    xs = [(torch.randn(B, Hkv, S, D, device=dev, generator=gen) * 3).to(dt) for _ in range(nbuf)]
+    pk = [torch.empty(B, Hkv, S, W_, device=dev, dtype=torch.uint8) for _ in range(nbuf)]
+    sc = [torch.empty(B, Hkv, S, NG, device=dev, dtype=dt) for _ in range(nbuf)]
+    outs = [torch.empty(B, Hkv, S, D, device=dev, dtype=dt) for _ in range(nbuf)]
+
+    def quant_round():
+        for j in range(nbuf):
+            ops.quantize_into(xs[j], pk[j], sc[j], G)
+
+    lib = ops.nat.lib()
+
+    def dequant_round():
+        # the kernel launch of ops.dequantize, into preallocated outputs
+        for j in range(nbuf):
+            rc = lib.kvq_dequantize(
+                pk[j].data_ptr(), ops.nat.i64_array(pk[j].stride()[:3]),
+                sc[j].data_ptr(), ops.nat.DTYPE_CODE[dt], ops.nat.i64_array(sc[j].stride()[:3]),
+                B, Hkv, S, G, NG, outs[j].data_ptr(), ops.nat.DTYPE_CODE[dt], ops.nat.i64_array(outs[j].stride()),
+                D, stream.cuda_stream)
+            ops.nat.check(rc, "kvq_dequantize")
+
+    rounds = 4
+
+    def timed(fn) -> float:
+        with torch.cuda.stream(stream):
+            for _ in range(max(1, args.warmup)):
+                fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(rounds):
+                fn()
+        torch.cuda.synchronize()
+        reps = max(1, min(args.steps, 20))
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        with torch.cuda.stream(stream):  # a graph replays on the current stream
+            ev[0].record(stream)
+            for i in range(reps):
+                g.replay()
+                ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 / (rounds * nbuf) for i in range(reps)]
+        # µs per launch: the mean over every timed replay, and the range of the replays' means
+        return sum(per) / reps, min(per), max(per)
+
+    us_q, q_lo, q_hi = timed(quant_round)
+    us_dq, dq_lo, dq_hi = timed(dequant_round)
+    # round-trip sanity of the timed outputs: |dequant(quant(x)) - x| is half a
+    # scale step, plus the roundings of the stored scale and of the output
+    # (0.6 of a step bounds both)
+    x0 = xs[0].float().view(n, NG, G)
+    err = (outs[0].float().view(n, NG, G) - x0).abs().amax(-1)
+    rt_ok = bool((err <= sc[0].float().abs().view(n, NG) * 0.6).all().item())
+    if args.calib_copy_mib:
+        calibration_copy(args.calib_copy_mib, dev, stream)
+    gbs_q = (x_bytes + code_bytes) / (us_q * 1e-6) / 1e9
+    gbs_dq = (x_bytes + code_bytes) / (us_dq * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "INT4 quantize of a prompt's K (or V) rows, HBM GB/s", "value": round(gbs_q, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": max(1, min(args.steps, 20)), "warmup": args.warmup, "us_per_launch": round(us_q, 3),
+        "us_per_launch_range": [round(q_lo, 3), round(q_hi, 3)],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
+        "data": "synthetic (seeded torch.randn * 3)",
+        "config": {"workload": f"{w['desc'].replace('decode', 'prompt-append')}", "shape": [B, Hkv, S, D],
+                   "group_size": G, "rotating_buffers": nbuf},
+        "roofline": {"bound": "hbm", "achieved": round(gbs_q, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs_q / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "quantize_vec_kernel",
+                     "bytes_per_launch": x_bytes + code_bytes},
+        "dequantize": {"gbs": round(gbs_dq, 1), "us_per_launch": round(us_dq, 3),
+                       "us_per_launch_range": [round(dq_lo, 3), round(dq_hi, 3)],
+                       "frac": round(gbs_dq / HBM_PEAK_GBS, 4), "kernel": "dequantize_vec_kernel"},
+        "round_trip_within_half_scale": rt_ok,
+    }), flush=True)
+    return 0 if rt_ok else 1
+
+
 def model_bench(args) -> int:
     """Whole-model decode at the C3 configuration: random-init Llama-3.1-8B in
     bf16 (weights ~N(0, 0.02) from the HF initialiser, seed 2), a 16384-token
@@ -898,7 +1007,8 @@ def summarize_pmc(fetch_csv: str, write_csv: str, calib_mib: int, cmd: str, matc
         expect_kib = calib_mib * 1024.0
         factor = expect_kib / cv if cv > 0 else float("nan")
         res[counter] = av * factor
-        out.append(f"{counter}: attention {av:.1f} KiB/dispatch (median of {ad}; {an[:80]})")
+        out.append(f"{counter}: {'attention' if 'attn' in match else 'kernel'} {av:.1f} KiB/dispatch "
+                   f"(median of {ad}; {an[:80]})")
         out.append(f"{counter}: calibration copy {cv:.1f} KiB/dispatch for {expect_kib:.0f} KiB moved "
                    f"(median of {cd}; {cn[:80]}) -> factor {factor:.4f}")
     total = (res["FETCH_SIZE"] + res["WRITE_SIZE"]) * 1024.0
