@@ -776,8 +776,9 @@ def quantize_bench(args, w: dict) -> int:
     Bytes per launch: the input read plus codes and scales written (quantize),
     codes and scales read plus the output written (dequantize). Enough
     buffers rotate that one round exceeds the 256 MB Infinity Cache; the
-    launches are captured in a HIP graph and timed with events on the launch
-    stream."""
+    launches are captured in a HIP graph, replayed untimed at least 40 times,
+    then timed with events on the launch stream (mean per launch over the
+    timed replays, and their range)."""
     import math
 
     import torch
@@ -829,6 +830,13 @@ def quantize_bench(args, w: dict) -> int:
         with torch.cuda.graph(g, stream=stream):
             for _ in range(rounds):
                 fn()
+        torch.cuda.synchronize()
+        # At least 40 untimed replays (tens of ms of launches): for the first
+        # tens of ms of sustained launches after an idle period these kernels
+        # run up to 40 % slower, on this part, than in the steady state after.
+        with torch.cuda.stream(stream):
+            for _ in range(max(40, args.warmup)):
+                g.replay()
         torch.cuda.synchronize()
         reps = max(1, min(args.steps, 20))
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
