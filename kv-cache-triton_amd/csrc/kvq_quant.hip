@@ -108,6 +108,15 @@ __global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
 // have unit inner stride and 16-byte aligned starts, and packed rows are
 // 4-byte aligned; everything else takes quantize_kernel.
 
+// The vector kernels stream every byte once, so their bulk accesses carry
+// the nontemporal hint (the `nt` bit): the quantizer's input loads and code
+// stores, and the dequantizer's output stores. Measured on prompt appends of
+// [1, 8, 16384, 128] and [8, 8, 32768, 128] bf16: quantize 14.0 -> 12.7 and
+// 135 -> 131 us a launch, dequantize 12.3 -> 9.7 and 122 -> 117 us. (The
+// dequantizer's code loads gained nothing from it; the decode kernels' cache
+// loads lost with it at large batch, and keep the default policy.)
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
@@ -158,7 +167,8 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     const int64_t xoff = (int64_t)bb[k] * a.xs_b + (int64_t)hh[k] * a.xs_h + (int64_t)ss[k] * a.xs_s + 8 * ch;
 #pragma unroll
     for (int n = 0; n < NW; ++n)
-      raw[k][n] = *(const uint4*)((const uint8_t*)a.x + (xoff + 4 * n) * (NW * 2));
+      raw[k][n] = __builtin_bit_cast(
+          uint4, __builtin_nontemporal_load((const nt_u32x4*)((const uint8_t*)a.x + (xoff + 4 * n) * (NW * 2))));
   }
   int64_t pos[RPT];
   if (a.write_pos) {
@@ -256,7 +266,7 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(const QuantArgs a) {
     const int64_t b = bb[k], h = hh[k], pos = dst[k];
     if (pos < 0) continue;  // no destination row
     // chunk ch covers bytes [4 ch, 4 ch + 4) of the packed row (G even, no padding)
-    *(uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch) = word;
+    __builtin_nontemporal_store(word, (uint32_t*)(a.packed + b * a.ps_b + h * a.ps_h + pos * a.ps_s + 4 * ch));
     if (ch % LPG == 0) {
       const int64_t g = ch / LPG;
       store_from_f32(a.scales, b * a.ss_b + h * a.ss_h + pos * a.ss_s + g, a.scale_dtype, scale);
@@ -384,7 +394,7 @@ __global__ __launch_bounds__(256) void dequantize_vec_kernel(const DequantArgs a
           p[j] = __builtin_bit_cast(uint32_t, h);
         }
       }
-      *(uint4*)((uint16_t*)a.out + o) = make_uint4(p[0], p[1], p[2], p[3]);
+      __builtin_nontemporal_store(nt_u32x4{p[0], p[1], p[2], p[3]}, (nt_u32x4*)((uint16_t*)a.out + o));
     }
   }
 }
