@@ -355,7 +355,7 @@ def main() -> int:
         result["roofline"]["ceiling"] = {
             "achieved": best["gbs"], "unit": "GB/s", "frac_of_peak": round(best["gbs"] / HBM_PEAK_GBS, 4),
             "decode_frac_of_ceiling": round(achieved / best["gbs"], 4), "grid": best["grid"],
-            "block": best["block"], "kernarg_preload": best["preload"],
+            "block": best["block"], "kernarg_preload": best["preload"], "nontemporal": best["nt"],
             "kernel": "stream_read (libkvq_probe.so)",
         }
     if not args.no_cpu_baseline:
@@ -442,7 +442,7 @@ def probe_lib():
         fn = getattr(lib, name)
         fn.restype = getattr(prod, name).restype
         fn.argtypes = getattr(prod, name).argtypes
-    for name in ("kvq_probe_stream_read", "kvq_probe_stream_read_preload"):
+    for name in ("kvq_probe_stream_read", "kvq_probe_stream_read_preload", "kvq_probe_stream_read_preload_nt"):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
@@ -460,8 +460,8 @@ def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
     launch per buffer captured in a HIP graph and replayed 20 times between
     two events on the launch stream: per (grid, block) and per build of the
     read (preload False: the wave loads its arguments from memory; True: the
-    hardware preloads them into SGPRs), the average launch time and GB/s over
-    nbytes."""
+    hardware preloads them into SGPRs; nt: preloaded, and the loads carry the
+    nontemporal hint), the average launch time and GB/s over nbytes."""
     import torch
 
     lib = probe_lib()
@@ -470,12 +470,13 @@ def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
     bufs = [torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev, generator=g) for _ in range(L)]
     sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)  # >= any grid below (one word per workgroup)
     out = []
-    for (grid, block), preload in ((gb, pl) for gb in grids for pl in (False, True)):
+    for (grid, block), (preload, nt) in ((gb, v) for gb in grids for v in ((False, False), (True, False), (True, True))):
         # larger buffers: more workgroups, so that each thread keeps at most
         # 20 pieces in flight (no register spills)
         while -(-(n // 16) // (grid * block)) > 20:
             grid *= 2
-        read = lib.kvq_probe_stream_read_preload if preload else lib.kvq_probe_stream_read
+        read = (lib.kvq_probe_stream_read_preload_nt if nt else
+                lib.kvq_probe_stream_read_preload if preload else lib.kvq_probe_stream_read)
         graph = torch.cuda.CUDAGraph()
         per = 0
         with torch.cuda.graph(graph, stream=stream):
@@ -495,7 +496,7 @@ def stream_ceiling(nbytes: int, L: int, dev, stream, grids, keep=None) -> list:
             e1.record(stream)
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / (20 * L)
-        out.append({"grid": grid, "block": block, "preload": preload, "pieces_per_thread": per,
+        out.append({"grid": grid, "block": block, "preload": preload, "nt": nt, "pieces_per_thread": per,
                     "us_per_launch": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
     if keep is not None:
         keep.extend(bufs)
@@ -1071,7 +1072,7 @@ def summarize_probe(path: str) -> str:
     out = [f"streaming read of {d['bytes_per_launch']} B per launch, {d['layers']} buffers, graph of "
            f"{d['layers']} launches x 20 replays:"]
     for r in d["stream"]:
-        pl = "preloaded args" if r.get("preload") else "args from memory"
+        pl = ("preloaded, nt" if r.get("nt") else "preloaded args") if r.get("preload") else "args from memory"
         out.append(f"  grid {r['grid']:5d} x {r['block']:4d}  {r['pieces_per_thread']:2d} x 16 B per thread  "
                    f"{pl:<16}  {r['us_per_launch']:7.3f} us/launch  {r['gbs']:7.1f} GB/s")
     for r in d.get("issue_cost", []):

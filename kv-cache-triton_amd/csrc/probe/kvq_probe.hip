@@ -6,14 +6,20 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// Built twice into the library: as is, and with KVQ_PROBE_PRELOAD defined and
-// -amdgpu-kernarg-preload-count, which has the hardware load the kernels'
-// scalar arguments into SGPRs at wave launch. The second build's kernels live
-// in namespace kvq_probe_pl and its entry points carry the suffix _preload.
-// Preload lets a wave issue its loads without first waiting for the argument
-// block to arrive from memory (it helps reads of a few MB and more), but costs
-// the smallest launches a little, so the ceiling takes the best of both.
-#if defined(KVQ_PROBE_PRELOAD)
+// Built three times into the library: as is; with KVQ_PROBE_PRELOAD defined
+// and -amdgpu-kernarg-preload-count, which has the hardware load the kernels'
+// scalar arguments into SGPRs at wave launch (namespace kvq_probe_pl, entry
+// points suffixed _preload); and with KVQ_PROBE_NT defined as well, where
+// stream_read's loads carry the nontemporal hint (namespace kvq_probe_pl_nt,
+// suffix _preload_nt). Preload lets a wave issue its loads without first
+// waiting for the argument block to arrive from memory (it helps reads of a
+// few MB and more), but costs the smallest launches a little. The hint lets
+// the hardware stream lines that one instruction reads whole; it helps large
+// reads most. The ceiling takes the best of the three.
+#if defined(KVQ_PROBE_PRELOAD) && defined(KVQ_PROBE_NT)
+#define KVQ_PROBE_NS kvq_probe_pl_nt
+#define KVQ_PROBE_FN(name) name##_preload_nt
+#elif defined(KVQ_PROBE_PRELOAD)
 #define KVQ_PROBE_NS kvq_probe_pl
 #define KVQ_PROBE_FN(name) name##_preload
 #else
@@ -28,6 +34,16 @@ namespace KVQ_PROBE_NS {
 // before the first is used, and folds them with XOR. Nothing is written
 // unless the fold equals a value no test buffer produces, so the kernel's
 // traffic is the buffer's bytes.
+typedef uint32_t probe_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 read16(const uint4* p) {
+#if defined(KVQ_PROBE_NT)
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const probe_u32x4*)p));
+#else
+  return *p;
+#endif
+}
+
 template <int PER>
 __global__ __launch_bounds__(1024) void stream_read(const uint4* __restrict__ p, uint64_t n16, uint32_t* sink) {
   const uint64_t t = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
@@ -36,7 +52,7 @@ __global__ __launch_bounds__(1024) void stream_read(const uint4* __restrict__ p,
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const uint64_t j = t + i * T;
-    v[i] = j < n16 ? p[j] : make_uint4(0u, 0u, 0u, 0u);
+    v[i] = j < n16 ? read16(p + j) : make_uint4(0u, 0u, 0u, 0u);
   }
   uint32_t acc = 0;
 #pragma unroll
