@@ -113,6 +113,10 @@ def main() -> int:
                          "WRITE_SIZE run of this script with --calib-copy-mib) into a traffic summary on stdout")
     ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
                     help="no GPU work: turn a rocprofv3 --kernel-trace --stats kernel_stats.csv into a summary")
+    ap.add_argument("--trace-csv", metavar="KERNEL_TRACE_CSV", default="",
+                    help="with --summarize-trace: the run's kernel_trace.csv, for the average over the last "
+                         "--trace-tail dispatches of the decode kernel (the bench's timed attention graph)")
+    ap.add_argument("--trace-tail", type=int, default=640, help="dispatches averaged by --trace-csv")
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="no GPU work: per-dispatch, per-wave and per-tile medians of the decode kernel's "
                          "counters in a rocprofv3 --pmc counter_collection.csv")
@@ -133,7 +137,8 @@ def main() -> int:
                             args.kernel_match))
         return 0
     if args.summarize_trace:
-        print(summarize_trace(args.summarize_trace, args.cmd))
+        print(summarize_trace(args.summarize_trace, args.cmd, args.trace_csv, args.trace_tail,
+                              args.kernel_match))
         return 0
     if args.summarize_probe:
         print(summarize_probe(args.summarize_probe))
@@ -1100,9 +1105,15 @@ def summarize_probe(path: str) -> str:
     return "\n".join(out)
 
 
-def summarize_trace(stats_csv: str, cmd: str) -> str:
+def summarize_trace(stats_csv: str, cmd: str, trace_csv: str = "", tail: int = 640,
+                    match: str = "decode_attn_") -> str:
     """Per-kernel call count and average / min / max duration from a rocprofv3
-    --stats kernel_stats.csv, kvq kernels first."""
+    --stats kernel_stats.csv, kvq kernels first. With the run's
+    kernel_trace.csv, also the average over the last `tail` dispatches of the
+    kernel (name containing `match`) with the most dispatches: in a bench.py
+    run those are its timed attention-graph replays (steps x layers launches),
+    the launches its roofline figure averages; the whole-run average also
+    holds eager warm-up launches and the step graph's replays."""
     import csv
 
     rows = list(csv.DictReader(open(stats_csv)))
@@ -1112,6 +1123,18 @@ def summarize_trace(stats_csv: str, cmd: str) -> str:
     for r in rows[:12]:
         out.append(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.3f} {float(r['MinNs']) / 1e3:9.3f} "
                    f"{float(r['MaxNs']) / 1e3:9.3f} {float(r['Percentage']):6.2f}  {r['Name'][:110]}")
+    if trace_csv:
+        disp: dict = {}
+        for r in csv.DictReader(open(trace_csv)):
+            if match in r["Kernel_Name"]:
+                disp.setdefault(r["Kernel_Name"], []).append(
+                    (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+        if disp:
+            name, ds = max(disp.items(), key=lambda kv: len(kv[1]))
+            ds.sort()
+            last = [d for _, d in ds[-tail:]]
+            out.append(f"last {len(last)} of {len(ds)} dispatches of {name[:80]}: average "
+                       f"{sum(last) / len(last) / 1e3:.3f} us (min {min(last) / 1e3:.3f}, max {max(last) / 1e3:.3f})")
     return "\n".join(out)
 
 
