@@ -782,7 +782,12 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   // about half the time instead of both arriving late together (north star
   // 9.50 -> 9.45 us, C4 62.1 -> 61.6 us; outputs bit-identical).
   if (wave < NW / 2) __builtin_amdgcn_s_setprio(1);
-  fetch_prologue_args(a);
+  // The paged one-row-set kernel at D = 128 skips the early fetch: with the
+  // block-table state on top, holding all those arguments made it spill 15
+  // scalar registers to VGPR lanes (and reload them over 100 times); without
+  // the fetch it spills 2, and the paged north star went 10.95 -> 10.64 us.
+  // The other paged kernels lost without it (C5 paged 10.40 -> 10.63 us).
+  if constexpr (!(PAGED && D == 128 && RS == 1)) fetch_prologue_args(a);
   // One field of each of the argument block's last two 64-byte lines in the
   // first batch as well, so that both lines are in the scalar cache before
   // anything else reads them: the block table (paged kernels) before the first
