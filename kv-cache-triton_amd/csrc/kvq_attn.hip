@@ -776,12 +776,6 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   KVQ_STAMP(0);
-  // The two waves of a SIMD (w and w + 4) run the same scalar prologue, and a
-  // SIMD issues one scalar instruction per turn: raising the first one's
-  // priority until its first tiles' loads are issued lets it reach them in
-  // about half the time instead of both arriving late together (north star
-  // 9.50 -> 9.45 us, C4 62.1 -> 61.6 us; outputs bit-identical).
-  if (wave < NW / 2) __builtin_amdgcn_s_setprio(1);
   // The paged one-row-set kernel at D = 128 skips the early fetch: with the
   // block-table state on top, holding all those arguments made it spill 15
   // scalar registers to VGPR lanes (and reload them over 100 times); without
@@ -797,6 +791,21 @@ void decode_attn_mfma_kernel(const AttnArgs a) {
   asm volatile("" ::"s"(a.bt_cols), "s"(a.ws_o));
   int unit, split;
   if (!unit_and_split(a, unit, split)) return;
+  // The two waves of a SIMD (w and w + 4) run the same scalar prologue, and a
+  // SIMD issues one scalar instruction per turn: raising the first one's
+  // priority until its first tiles' loads are issued lets it reach them in
+  // about half the time instead of both arriving late together (north star
+  // 9.50 -> 9.45 us, C4 62.1 -> 61.6 us; outputs bit-identical). In the
+  // split that appends the new token, the one-row-set kernel at D = 128 gives
+  // the priority to the two appending waves (NW - 2, NW - 1) instead of their
+  // partners: their extra work (the new token's quantize, store and score)
+  // sets the end of that split, which the merge waits for (north star
+  // 9.33 -> 9.26 us, C2 7.27 -> 7.29 us; with four waves per SIMD, C5 lost
+  // 0.28 us that way).
+  {
+    const bool app = D == 128 && RS == 1 && a.append && split == a.n_split - 1 && (wave % (NW / 2)) >= NW / 2 - 2;
+    if ((wave < NW / 2) != app) __builtin_amdgcn_s_setprio(1);
+  }
   int b, kvh, rc;
   unit_coords(a, unit, b, kvh, rc);
   // the sequence's length is read first (its latency then overlaps the query
